@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark of the compressed-KV path on one MI355X.
+
+Workload (default c2a, the headline shape): Llama-3.1-8B attention, 32 query / 8 KV heads,
+head dim 128, batch 8 x 8,192 context, page 16, synthetic K/V of the configuration-0 recipe
+(RoPE'd keys with per-channel scales, 0.04% zeros, 0.3% raw rows). One step = one decode
+attention call (split kernel + merge) over the compressed cache, inputs resident in HBM.
+The Infinity Cache (256 MB) is defeated by rotating over several cache copies.
+
+Prints one JSON line: value = microseconds per call (lower is better), the roofline of the
+dominant kernel (the split kernel: algorithmic bytes / its average duration, HIP events on
+the launch stream), the bf16-uncompressed twin for comparison, the encoder's throughput,
+and the CPU baseline (the oracle codec decode + fp32 attention on the host, one thread,
+on a sample of the sequences, scaled to the full call).
+
+    python bench.py [--steps 50] [--warmup 10] [--workload c2a]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs & % HBM peak at 32q/8kv, 8×8K ctx; e2e greedy decode tok/s"
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {   # name: (B, T, TS, Hq, Hkv, description)
+    "c2a": (8, 8192, 8192, 32, 8, "Llama-3.1-8B decode attention 32q/8kv, B8 x 8192 ctx"),
+    "c2a_ragged": (8, 8185, 8192, 32, 8, "Llama-3.1-8B decode attention 32q/8kv, B8 x 8185 ctx (partial page)"),
+    "c2b": (1, 131072, 131072, 32, 8, "Llama-3.1-8B decode attention 32q/8kv, B1 x 131072 ctx"),
+    "c1": (1, 32768, 32768, 28, 4, "Qwen2.5-7B decode attention 28q/4kv, B1 x 32768 ctx"),
+}
+
+
+def cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def algorithmic_bytes(caches, B, T, Hq, Hkv):
+    """Bytes a decode-attention call must move: per K/V cache and valid token row
+    128 (sm) + 64 (code); per touched page and head 128 (base) + 8 (rowmask, rowoff);
+    256 per raw row referenced; plus q and the output."""
+    import torch
+    npg = -(-T // 16)
+    total = 0
+    for c in caches:
+        rm = c.rowmask[:B, :npg].to(torch.int64)
+        raw_rows = int(sum(((rm >> i) & 1).sum().item() for i in range(16)))
+        total += B * T * Hkv * 192 + B * npg * Hkv * 136 + raw_rows * 256
+    return total + 2 * B * Hq * 128 * 2
+
+
+def time_loop(fn, n, warmup, copies):
+    """Average ms per call of fn(i) over n calls, rotating over `copies` inputs, timed with
+    HIP events on the current stream (the stream every call launches on)."""
+    import torch
+    for i in range(warmup):
+        fn(i % copies)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(n):
+        fn(i % copies)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def cpu_baseline(kc, vc, q, B, T, nseq):
+    """The oracle (restated reference codec decode + fp32 GQA attention, numpy, 1 thread) on
+    the first `nseq` sequences; reported as microseconds for the full B-sequence call."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as oatt
+    from oracle import codec as ocodec
+
+    def host(c):
+        d = dict(shape=(nseq, c.TS, c.H, c.D))
+        for k in ("sm", "code", "base", "rowmask", "rowoff"):
+            d[k] = getattr(c, k)[:nseq].cpu().numpy()
+        d["raw"] = c.raw.cpu().view(torch.int16).numpy().view(np.uint16)
+        return d
+    hk, hv = host(kc), host(vc)
+    qh = q[:nseq].cpu().view(torch.int16).numpy().view(np.uint16)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        kd = ocodec.decode(hk, T)
+        vd = ocodec.decode(hv, T)
+        oatt.attention(qh, kd, vd, T, np.float32)
+        dt = time.perf_counter() - t0
+    return dict(value=round(dt * 1e6 * B / nseq, 1), unit="us", cores=1, kind="port",
+                sample=f"{nseq} of {B} sequences x {T} tokens: numpy codec decode of K and V + fp32 attention, "
+                       f"scaled x{B / nseq:g}", cpu=cpu_model(), seconds=round(dt, 2))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS))
+    ap.add_argument("--copies", type=int, default=4, help="cache copies rotated to defeat the 256 MB MALL")
+    ap.add_argument("--cpu-seqs", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--target-blocks", type=int, default=None)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
+              "(the decode path shards by KV head or sequence with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import exactkv_amd as exactkv
+    from exactkv_amd import kernels, synthetic
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
+    print(f"[bench] {a.workload}: {desc}; generating data", file=sys.stderr, flush=True)
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=100, device=dev)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=101, device=dev)
+    q = synthetic.make_q(B, Hq, seed=102, device=dev)
+    kcs, vcs, kbs, vbs = [], [], [], []
+    for i in range(a.copies):
+        kc, vc = exactkv.CompressedKV(B, TS, Hkv, 128), exactkv.CompressedKV(B, TS, Hkv, 128)
+        for b in range(B):
+            kc.prefill_slot(b, k[b:b + 1, :T])
+            vc.prefill_slot(b, v[b:b + 1, :T])
+        kcs.append(kc)
+        vcs.append(vc)
+        kbs.append(k.clone())
+        vbs.append(v.clone())
+    del k, v
+    torch.cuda.synchronize()
+    print("[bench] caches encoded", file=sys.stderr, flush=True)
+    ns, sl = kernels.plan_splits(B, Hkv, Hq, T, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
+    out = torch.empty_like(q)
+    o_c = kernels.attention_compressed(q, kcs[0], vcs[0], T, nsplit=ns, split_len=sl)
+    o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl)
+    identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
+
+    ms_c = time_loop(lambda i: kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl,
+                                                            out=out), a.steps, a.warmup, a.copies)
+    ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl,
+                                                           out=out), a.steps, a.warmup, a.copies)
+    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True), a.steps, a.warmup,
+                         a.copies)
+    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False), a.steps, a.warmup,
+                           a.copies)
+    print("[bench] attention timed", file=sys.stderr, flush=True)
+
+    alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv)
+    alg_b = 2 * B * T * Hkv * 256 + 2 * B * Hq * 128 * 2
+    gbps = alg / (ms_split * 1e-3) / 1e9
+    enc = encoder_gbps(exactkv, kernels, kbs[0], T, a.steps, a.warmup)
+    print("[bench] encoder timed", file=sys.stderr, flush=True)
+
+    res = {
+        "metric": METRIC, "value": round(ms_c * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms_c, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{a.workload}: {desc}", "B": B, "T": T, "TS": TS, "Hq": Hq, "Hkv": Hkv,
+                   "head_dim": 128, "page": 16, "nsplit": ns, "split_len": sl, "cache_copies": a.copies,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
+                     "kernel_us": round(ms_split * 1e3, 2)},
+        "bf16_twin_us": round(ms_b * 1e3, 2),
+        "bf16_split_us": round(ms_split_b * 1e3, 2),
+        "bf16_split_GBps": round(alg_b / (ms_split_b * 1e-3) / 1e9, 1),
+        "speedup_vs_bf16": round(ms_b / ms_c, 3),
+        "bit_identical_to_bf16": bool(identical),
+        "bits_per_value": round((kcs[0].nbytes() + vcs[0].nbytes()) * 8 / (2 * B * TS * Hkv * 128), 3),
+        "encoder_GBps": enc,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    if not a.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, min(a.cpu_seqs, B))
+        print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
+    print(json.dumps(res), flush=True)
+
+
+def split_only(kernels, q, kc, vc, T, ns, sl, compressed):
+    """Launch only the split kernel (the dominant kernel) into the shared workspace."""
+    from exactkv_amd import _lib
+    B, Hq, D = q.shape
+    wo, wm, wl = kernels._workspace(q.device, B * Hq, ns)
+    scale = D ** -0.5 * kernels.LOG2E
+    if compressed:
+        ka, TS, Hkv, _ = kernels._cache_args(kc)
+        va, _, _, _ = kernels._cache_args(vc)
+        _lib.call("exkv_attn_split_compressed", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, None, 0, ns, sl, scale, _lib.stream())
+    else:
+        TS, Hkv = kc.shape[1], kc.shape[2]
+        _lib.call("exkv_attn_split_bf16", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), wo.data_ptr(), wm.data_ptr(),
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, None, 0, ns, sl, scale, _lib.stream())
+
+
+def encoder_gbps(exactkv, kernels, x, T, steps, warmup):
+    """Page-encoder throughput on one prefill of the workload's keys: (bf16 read + compressed
+    write) bytes / time."""
+    import torch
+    B, TS, H, D = x.shape
+    npg = T // 16
+    c = exactkv.CompressedKV(B, TS, H, D, reserve=0.05)
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+
+    def enc(_):
+        c.cnt.zero_()
+        kernels.encode_pages(x, st, c._buf(), 0, 0, B, npg)
+    ms = time_loop(enc, max(5, steps // 5), max(2, warmup // 5), 1)
+    nraw = int(c.cnt.item())
+    rows = B * npg * 16 * H
+    byts = rows * 256 + rows * 192 + B * npg * H * 136 + nraw * 256
+    return round(byts / (ms * 1e-3) / 1e9, 1)
+
+
+if __name__ == "__main__":
+    main()

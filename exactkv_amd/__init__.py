@@ -1,0 +1,23 @@
+"""exactkv on MI355X: a lossless (bit-exact) compressed KV cache for LLM decoding, with
+decode attention that reads the compressed cache directly -- hand-written HIP kernels
+for gfx950 behind the reference's Python API (drop-in for zyfyz666/exactkv's names).
+
+    import exactkv_amd as exactkv
+"""
+from .cache import CompressedKV, BF16KV, check_overflow
+from .attention import decode_attention
+from .codec import encode_reference, decode_reference, bits_per_value
+from .kernels import attention_compressed, attention_reference, decode_to_bf16, encode_pages
+
+
+def __getattr__(name):
+    if name == "Engine":                 # imports transformers-side helpers lazily
+        from .engine import Engine
+        return Engine
+    raise AttributeError(name)
+
+
+__version__ = "0.1.0"
+__all__ = ["CompressedKV", "BF16KV", "check_overflow", "decode_attention", "Engine",
+           "encode_reference", "decode_reference", "bits_per_value",
+           "attention_compressed", "attention_reference", "decode_to_bf16", "encode_pages"]

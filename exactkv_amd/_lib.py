@@ -1,0 +1,91 @@
+"""ctypes binding of libexactkv_hip.so (the C-ABI declared in include/exactkv.h).
+
+The library is loaded on first use, after torch (so that it binds to the HIP runtime
+torch has loaded). There is no fallback: every compute entry point raises if the
+library is missing or a call fails.
+"""
+import ctypes
+import os
+
+_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
+ABI_VERSION = 1
+
+_p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+
+# name -> argument types (every entry point returns int: 0 ok, 1 bad argument, 2 HIP error)
+SIGNATURES = {
+    "exkv_encode_pages": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_cache_append": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
+                          _i32, _p],
+    "exkv_bf16_append": [_p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _p],
+    "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p,
+                             _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
+    "exkv_attn_bf16": [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
+                       _f32, _p],
+    "exkv_attn_split_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p,
+                                   _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
+    "exkv_attn_split_bf16": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
+                             _f32, _p],
+    "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
+    "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
+    "exkv_abi_version": [],
+    "exkv_last_error": [],
+}
+
+_lib = None
+
+
+def path():
+    return _PATH
+
+
+def load():
+    """Load the library (once). Raises RuntimeError if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_PATH):
+        raise RuntimeError(f"exactkv HIP library not found at {_PATH}; build it with "
+                           "`python -m exactkv_amd.build` (or __graft_entry__.build())")
+    import torch  # noqa: F401  -- torch's HIP runtime must be loaded before the library
+    lib = ctypes.CDLL(_PATH)
+    for name, args in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = ctypes.c_char_p if name == "exkv_last_error" else ctypes.c_int
+    v = lib.exkv_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"libexactkv_hip.so ABI version {v}, expected {ABI_VERSION}: rebuild the library")
+    runtimes = {ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64" in ln}
+    if len(runtimes) > 1:
+        raise RuntimeError(f"two HIP runtimes loaded in one process: {sorted(runtimes)}")
+    _lib = lib
+    return lib
+
+
+def call(name, *args):
+    """Call entry point `name`; raise RuntimeError with the library's message on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.exkv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t, align=16, what="tensor"):
+    """Device pointer of a CUDA (HIP) tensor, checked for device and alignment."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be on the GPU (got {t.device})")
+    p = t.data_ptr()
+    if align and p % align:
+        raise ValueError(f"{what} is not {align}-byte aligned")
+    return p

@@ -1,0 +1,92 @@
+// Shared definitions for the exactkv HIP kernels (gfx950 / CDNA4).
+//
+// Byte format (reference exactkv/codec.py:1-25): per (sequence, 16-token page, KV head,
+// channel) one base byte; per element a sign|mantissa byte and a 4-bit exponent code,
+// where code byte j of a row holds channel j (low nibble) and channel j + 64 (high
+// nibble). base < 128: exponent = base + code. base >= 128 (a group with zeros):
+// code 0 means exponent 0, otherwise exponent = base - 128 + code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exkv {
+
+constexpr int kPage = 16;     // tokens per page
+constexpr int kD = 128;       // head dimension (the only one the format supports)
+
+// ---------------------------------------------------------------- bit helpers
+
+// v_perm_b32: byte i of the result = byte sel.byte[i] of the 8-byte value {hi, lo}
+// (bytes 0-3 from lo, 4-7 from hi; selector 12 gives 0x00).
+__host__ __device__ inline uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_perm(hi, lo, sel);
+#else
+    uint64_t v = ((uint64_t)hi << 32) | lo;
+    uint32_t r = 0;
+    for (int i = 0; i < 4; ++i) {
+        uint32_t s = (sel >> (8 * i)) & 0xFF;
+        uint32_t b = s < 8 ? (uint32_t)((v >> (8 * s)) & 0xFF) : (s == 12 ? 0u : 0xFFu);
+        r |= b << (8 * i);
+    }
+    return r;
+#endif
+}
+
+// (m & a) | (~m & b): one v_bfi_b32.
+__host__ __device__ inline uint32_t bfi_b32(uint32_t m, uint32_t a, uint32_t b) {
+    return (m & a) | (~m & b);
+}
+
+// ---------------------------------------------------------------- value rebuild
+//
+// Four consecutive channels at once. s: their sign|mantissa bytes; cn: their 4-bit
+// codes, one per byte (0..15); bm: their base bytes with the zero flag cleared
+// (0..127); zf: their base bytes' zero flags (0x80 per byte, 0 elsewhere).
+// Result: two dwords of bf16 pairs (channel c in the low half, c + 1 in the high half),
+// bit-identical to the reference decoder (codec.py:65-68, kernels.py:96-103).
+//
+// exponent e = bm + code (<= 142, so the bytewise add never carries). The bf16 is
+// hi byte = (s & 0x80) | (e >> 1), lo byte = (e & 1) << 7 | (s & 0x7F).
+__host__ __device__ inline uint32_t zero_mask(uint32_t cn, uint32_t zf) {
+    // bit 7 of each byte of cn + 0x7F is set iff code >= 1 (code <= 15: no carry out)
+    uint32_t z80 = zf & ~(cn + 0x7F7F7F7Fu);
+    // 0x80 -> 0xFF per flagged byte: (z << 1) - (z >> 7) sets exactly those bytes
+    return (z80 << 1) - (z80 >> 7);
+}
+
+template <bool HAS_ZERO_GROUPS>
+__host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t bm, uint32_t zf,
+                                         uint32_t& out01, uint32_t& out23) {
+    uint32_t e = cn + bm;
+    if (HAS_ZERO_GROUPS) e &= ~zero_mask(cn, zf);
+    uint32_t lo = bfi_b32(0x7F7F7F7Fu, s, e << 7);
+    uint32_t hi = bfi_b32(0x80808080u, s, e >> 1);
+    out01 = perm_b32(hi, lo, 0x05010400u);
+    out23 = perm_b32(hi, lo, 0x07030602u);
+}
+
+// ---------------------------------------------------------------- small device utils
+
+__device__ inline int popc32(uint32_t x) { return __builtin_popcount(x); }
+
+}  // namespace exkv
+
+// ---------------------------------------------------------------- C-ABI error plumbing
+namespace exkv {
+void set_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* where);
+}  // namespace exkv
+
+#define EXKV_OK 0
+#define EXKV_E_ARG 1
+#define EXKV_E_HIP 2
+
+#define EXKV_REQUIRE(cond, ...)                  \
+    do {                                         \
+        if (!(cond)) {                           \
+            exkv::set_error(__VA_ARGS__);        \
+            return EXKV_E_ARG;                   \
+        }                                        \
+    } while (0)

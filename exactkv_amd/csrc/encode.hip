@@ -1,0 +1,401 @@
+// Page encoder, deterministic raw-slot assignment, device-side append and the
+// compressed -> bf16 decoder, for gfx950.
+//
+// Encoding one call's pages takes three launches on the caller's stream:
+//   1. enc_pages_kernel  one wavefront per (sequence, page, head): exponent window,
+//                        zero flag, codes, sign|mantissa bytes, base bytes, rowmask
+//                        (reference kernels.py:216-264, codec.py:31-49);
+//   2. scan_kernel       one workgroup: rowoff = counter + exclusive running count of raw
+//                        rows over the call's pages in (sequence, page, head) order; the
+//                        counter advances by the total (codec.py:50-53 order; the
+//                        reference GPU encoder used an atomic counter, kernels.py:262);
+//   3. rawcopy_kernel    copies raw rows into their slots, skipping slots >= cap
+//                        (kernels.py:265-268), so an overflow is seen from the counter.
+// The append path (cache.py:100-112) runs the same three steps with the token count
+// read from device memory, so a decode step can be captured in a HIP graph.
+#include "tile.hpp"
+#include "../../include/exactkv.h"
+
+namespace exkv {
+
+__device__ inline uint8_t sm_byte(uint32_t u) { return (uint8_t)(((u >> 8) & 0x80u) | (u & 0x7Fu)); }
+
+// Encode one 16-token page of one head. Lane l owns channels l and l + 64, so a code
+// byte (channel j low nibble, j + 64 high nibble) is produced by one lane. Token p's
+// source row is src + p * s_p, except row 15 which comes from `last` when given.
+// Destination rows of consecutive tokens are `rs` rows apart (rs = H).
+__device__ void encode_page(const uint16_t* src, int64_t s_p, const uint16_t* last, int lane,
+                            uint8_t* sm0, uint8_t* code0, int64_t rs, uint8_t* basep, int32_t* rmaskp) {
+    uint32_t ulo[kPage], uhi[kPage];
+#pragma unroll
+    for (int p = 0; p < kPage; ++p) {
+        const uint16_t* rp = (p == kPage - 1 && last != nullptr) ? last : src + p * s_p;
+        ulo[p] = rp[lane];
+        uhi[p] = rp[lane + 64];
+    }
+    int top_lo = 0, top_hi = 0;
+    bool z_lo = false, z_hi = false;
+#pragma unroll
+    for (int p = 0; p < kPage; ++p) {
+        const int el = (ulo[p] >> 7) & 255, eh = (uhi[p] >> 7) & 255;
+        top_lo = max(top_lo, el);
+        top_hi = max(top_hi, eh);
+        z_lo |= el == 0;
+        z_hi |= eh == 0;
+    }
+    const int fl_lo = max(top_lo - 15, 0), fl_hi = max(top_hi - 15, 0);
+    const bool zf_lo = z_lo && fl_lo > 0, zf_hi = z_hi && fl_hi > 0;
+    uint32_t esc = 0;
+#pragma unroll
+    for (int p = 0; p < kPage; ++p) {
+        const int el = (ulo[p] >> 7) & 255, eh = (uhi[p] >> 7) & 255;
+        const int cl = (zf_lo && el == 0) ? 0 : el - fl_lo;
+        const int ch = (zf_hi && eh == 0) ? 0 : eh - fl_hi;
+        const bool ok_lo = fl_lo < 128 && cl >= ((zf_lo && el != 0) ? 1 : 0);
+        const bool ok_hi = fl_hi < 128 && ch >= ((zf_hi && eh != 0) ? 1 : 0);
+        esc |= (uint32_t)!(ok_lo && ok_hi) << p;
+        uint8_t* sp = sm0 + p * rs * 128;
+        sp[lane] = sm_byte(ulo[p]);
+        sp[lane + 64] = sm_byte(uhi[p]);
+        const int nl = min(max(cl, 0), 15), nh = min(max(ch, 0), 15);
+        code0[p * rs * 64 + lane] = (uint8_t)(nl | (nh << 4));
+    }
+    basep[lane] = (uint8_t)min(fl_lo + (zf_lo ? 128 : 0), 255);
+    basep[lane + 64] = (uint8_t)min(fl_hi + (zf_hi ? 128 : 0), 255);
+    uint32_t rm = 0;
+#pragma unroll
+    for (int p = 0; p < kPage; ++p)
+        if (__ballot((esc >> p) & 1u) != 0) rm |= 1u << p;
+    if (lane == 0) *rmaskp = (int32_t)rm;
+}
+
+struct EncArgs {
+    const uint16_t* src;
+    int64_t s_b, s_pg, s_p, s_h;      // source strides in elements
+    uint8_t* sm;
+    uint8_t* code;
+    uint8_t* base;
+    int32_t* rowmask;
+    int32_t* rowoff;
+    uint16_t* raw;
+    int32_t* cnt;
+    int32_t* before;
+    int64_t cap;
+    int b0, pg0, nb, npg, H, TS;
+};
+
+__device__ inline void unit_coords(const EncArgs& a, int64_t u, int& bi, int& pg, int& hk) {
+    hk = (int)(u % a.H);
+    const int64_t q = u / a.H;
+    pg = (int)(q % a.npg);
+    bi = (int)(q / a.npg);
+}
+
+__device__ inline int64_t unit_page(const EncArgs& a, int bi, int pg, int hk) {
+    return ((int64_t)(a.b0 + bi) * (a.TS / kPage) + (a.pg0 + pg)) * a.H + hk;
+}
+
+__global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunits) {
+    const int lane = threadIdx.x & 63;
+    const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= nunits) return;
+    int bi, pg, hk;
+    unit_coords(a, u, bi, pg, hk);
+    const uint16_t* src = a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h;
+    const int64_t row0 = ((int64_t)(a.b0 + bi) * a.TS + (int64_t)(a.pg0 + pg) * kPage) * a.H + hk;
+    const int64_t page = unit_page(a, bi, pg, hk);
+    encode_page(src, a.s_p, nullptr, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
+                a.rowmask + page);
+}
+
+// Block-wide exclusive scan of one int per thread (1024 threads).
+__device__ inline int block_excl_scan(int v, int& total) {
+    __shared__ int wsum[16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    int wpre = 0;
+    total = 0;
+    for (int i = 0; i < 16; ++i) {
+        const int s = wsum[i];
+        if (i < w) wpre += s;
+        total += s;
+    }
+    __syncthreads();
+    return wpre + inc - v;
+}
+
+__global__ void __launch_bounds__(1024) scan_kernel(EncArgs a, int64_t nunits) {
+    const int64_t per = (nunits + 1023) / 1024;
+    const int64_t u0 = threadIdx.x * per;
+    const int64_t u1 = min(u0 + per, nunits);
+    const int cnt0 = *a.cnt;
+    int local = 0;
+    for (int64_t u = u0; u < u1; ++u) {
+        int bi, pg, hk;
+        unit_coords(a, u, bi, pg, hk);
+        local += popc32((uint32_t)a.rowmask[unit_page(a, bi, pg, hk)]);
+    }
+    int total;
+    int run = cnt0 + block_excl_scan(local, total);
+    for (int64_t u = u0; u < u1; ++u) {
+        int bi, pg, hk;
+        unit_coords(a, u, bi, pg, hk);
+        const int64_t page = unit_page(a, bi, pg, hk);
+        a.rowoff[page] = run;
+        run += popc32((uint32_t)a.rowmask[page]);
+    }
+    if (threadIdx.x == 0) {
+        if (a.before) *a.before = cnt0;
+        *a.cnt = cnt0 + total;
+    }
+}
+
+// Copy one page's raw rows (token p's row at src + p*s_p) into slots rowoff + k (< cap).
+__device__ inline void copy_raw_rows(const uint16_t* src, int64_t s_p, uint32_t m, int32_t off, int64_t cap,
+                                     uint16_t* raw, int lane) {
+    int k = 0;
+    for (int p = 0; p < kPage; ++p) {
+        if (!((m >> p) & 1u)) continue;
+        const int64_t slot = (int64_t)off + k++;
+        if (slot >= cap) continue;
+        const uint16_t* s = src + p * s_p;
+        uint16_t* d = raw + slot * 128;
+        d[lane] = s[lane];
+        d[lane + 64] = s[lane + 64];
+    }
+}
+
+__global__ void __launch_bounds__(256) rawcopy_kernel(EncArgs a, int64_t nunits) {
+    const int lane = threadIdx.x & 63;
+    const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= nunits) return;
+    int bi, pg, hk;
+    unit_coords(a, u, bi, pg, hk);
+    const int64_t page = unit_page(a, bi, pg, hk);
+    const uint32_t m = (uint32_t)a.rowmask[page];
+    if (m == 0) return;
+    copy_raw_rows(a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, a.s_p, m, a.rowoff[page], a.cap, a.raw, lane);
+}
+
+// ---------------------------------------------------------------- device-side append
+
+struct AppendArgs {
+    const uint16_t* x;        // [B, H, 128] (row strides sx_b, sx_h in elements)
+    int64_t sx_b, sx_h;
+    uint8_t* sm;
+    uint8_t* code;
+    uint8_t* base;
+    int32_t* rowmask;
+    int32_t* rowoff;
+    uint16_t* raw;
+    int32_t* cnt;
+    int32_t* before;
+    int32_t* state;           // state[0] = tokens held (T)
+    int64_t cap;
+    int B, H, TS;
+};
+
+// Writes the new token into the tail area; when it completes a page, encodes that page
+// and opens the next one (rowmask all ones, rowoff into the tail area).
+__global__ void __launch_bounds__(256) append_write_kernel(AppendArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= a.B * a.H) return;
+    const int b = u / a.H, h = u % a.H;
+    const int T = a.state[0];
+    if (T < 0 || T >= a.TS) return;                // full cache: nothing is written
+    const int p = T % kPage;
+    uint16_t* tail = a.raw + (a.cap + (int64_t)u * kPage) * 128;
+    const uint16_t* x = a.x + b * a.sx_b + h * a.sx_h;
+    tail[p * 128 + lane] = x[lane];
+    tail[p * 128 + lane + 64] = x[lane + 64];
+    if (p != kPage - 1) return;
+    const int NP = a.TS / kPage;
+    const int pg = T / kPage;
+    const int64_t row0 = ((int64_t)b * a.TS + (int64_t)pg * kPage) * a.H + h;
+    const int64_t page = ((int64_t)b * NP + pg) * a.H + h;
+    encode_page(tail, 128, x, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
+                a.rowmask + page);
+    if (pg + 1 < NP && lane == 0) {
+        a.rowmask[page + a.H] = 0xFFFF;
+        a.rowoff[page + a.H] = (int32_t)(a.cap + (int64_t)u * kPage);
+    }
+}
+
+__global__ void __launch_bounds__(1024) append_scan_kernel(AppendArgs a) {
+    const int T = a.state[0];
+    if (T < 0 || T >= a.TS) return;
+    if (T % kPage == kPage - 1) {
+        const int NP = a.TS / kPage, pg = T / kPage;
+        const int n = a.B * a.H;
+        const int per = (n + 1023) / 1024;
+        const int u0 = threadIdx.x * per, u1 = min(u0 + per, n);
+        const int cnt0 = *a.cnt;
+        int local = 0;
+        for (int u = u0; u < u1; ++u)
+            local += popc32((uint32_t)a.rowmask[((int64_t)(u / a.H) * NP + pg) * a.H + u % a.H]);
+        int total;
+        int run = cnt0 + block_excl_scan(local, total);
+        for (int u = u0; u < u1; ++u) {
+            const int64_t page = ((int64_t)(u / a.H) * NP + pg) * a.H + u % a.H;
+            a.rowoff[page] = run;
+            run += popc32((uint32_t)a.rowmask[page]);
+        }
+        if (threadIdx.x == 0) {
+            *a.before = cnt0;
+            *a.cnt = cnt0 + total;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) a.state[0] = T + 1;
+}
+
+__global__ void __launch_bounds__(256) append_rawcopy_kernel(AppendArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= a.B * a.H) return;
+    const int T = a.state[0];
+    if (T % kPage != 0 || T <= 0 || T > a.TS) return;
+    const int NP = a.TS / kPage, pg = T / kPage - 1;
+    const int64_t page = ((int64_t)(u / a.H) * NP + pg) * a.H + u % a.H;
+    const uint32_t m = (uint32_t)a.rowmask[page];
+    if (m == 0) return;
+    copy_raw_rows(a.raw + (a.cap + (int64_t)u * kPage) * 128, 128, m, a.rowoff[page], a.cap, a.raw, lane);
+}
+
+// Plain bf16 cache (reference cache.py:129-146): buf[b, T, h] = x[b, h], T from device.
+__global__ void __launch_bounds__(256) bf16_append_kernel(const uint16_t* x, int64_t sx_b, int64_t sx_h,
+                                                          uint16_t* buf, const int32_t* state, int B, int H,
+                                                          int TS) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= B * H) return;
+    const int T = state[0];
+    if (T < 0 || T >= TS) return;
+    const int b = u / H, h = u % H;
+    uint16_t* d = buf + (((int64_t)b * TS + T) * H + h) * 128;
+    const uint16_t* s = x + b * sx_b + h * sx_h;
+    d[lane] = s[lane];
+    d[lane + 64] = s[lane + 64];
+}
+
+__global__ void bump_kernel(int32_t* state, int TS) {
+    if (state[0] < TS) state[0] += 1;
+}
+
+// ---------------------------------------------------------------- decode to bf16
+
+struct DecArgs {
+    CSrc c;
+    uint16_t* out;            // [B, T, H, 128]
+    int B, T, TS, H;
+};
+
+// One wavefront per (sequence, page, head), through the attention kernels' page decoder.
+__global__ void __launch_bounds__(256) decode_kernel(DecArgs a) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int NP = a.TS / kPage;
+    const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= (int64_t)a.B * NP * a.H) return;
+    const int h = (int)(u % a.H);
+    const int pg = (int)((u / a.H) % NP);
+    const int b = (int)(u / ((int64_t)a.H * NP));
+    if (pg * kPage >= a.T) return;
+    const int t = pg * kPage + r;
+    PageBytes pb;
+    load_page(a.c, ((int64_t)b * a.TS + t) * a.H + h, ((int64_t)b * NP + pg) * a.H + h, g, pb);
+    uint32_t v[16];
+    rebuild_page(a.c, pb, r, g, v);
+    if (t >= a.T) return;
+    uint4* o = reinterpret_cast<uint4*>(a.out + (((int64_t)b * a.T + t) * a.H + h) * 128 + 16 * g);
+    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
+    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    o[8] = make_uint4(v[8], v[9], v[10], v[11]);
+    o[9] = make_uint4(v[12], v[13], v[14], v[15]);
+}
+
+}  // namespace exkv
+
+using namespace exkv;
+
+static int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
+
+extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
+                                 void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
+                                 int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
+                                 int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
+                                 int32_t D, hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "encode_pages: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages: TS must be a positive multiple of 16 (got %d)", TS);
+    EXKV_REQUIRE(H > 0 && B > 0, "encode_pages: bad H=%d or B=%d", H, B);
+    EXKV_REQUIRE(nb >= 0 && npg >= 0 && b0 >= 0 && pg0 >= 0, "encode_pages: negative range");
+    EXKV_REQUIRE(b0 + nb <= B, "encode_pages: sequences [%d, %d) outside the cache (B=%d)", b0, b0 + nb, B);
+    EXKV_REQUIRE(pg0 + npg <= TS / kPage, "encode_pages: pages [%d, %d) outside the cache (%d pages)", pg0,
+                 pg0 + npg, TS / kPage);
+    EXKV_REQUIRE(cap >= 0 && cap <= raw_rows, "encode_pages: cap %lld exceeds the raw pool (%lld rows)",
+                 (long long)cap, (long long)raw_rows);
+    EXKV_REQUIRE(src && sm && code && base && rowmask && rowoff && raw && cnt, "encode_pages: null pointer");
+    const int64_t n = (int64_t)nb * npg * H;
+    if (n == 0) return EXKV_OK;
+    EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
+              rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
+    const unsigned grid = (unsigned)((n + 3) / 4);
+    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, a, n);
+    hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    return launch_status("encode_pages");
+}
+
+extern "C" int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
+                                 int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
+                                 int32_t* state, int64_t cap, int64_t raw_rows, int32_t B, int32_t H,
+                                 int32_t TS, int32_t D, hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "append: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(TS > 0 && TS % kPage == 0 && B > 0 && H > 0, "append: bad shape B=%d H=%d TS=%d", B, H, TS);
+    EXKV_REQUIRE(cap >= 0 && cap + (int64_t)B * H * kPage <= raw_rows,
+                 "append: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
+    EXKV_REQUIRE(x && sm && code && base && rowmask && rowoff && raw && cnt && before && state,
+                 "append: null pointer");
+    AppendArgs a{(const uint16_t*)x, sx_b, sx_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base, rowmask, rowoff,
+                 (uint16_t*)raw, cnt, before, state, cap, B, H, TS};
+    const unsigned grid = (unsigned)((B * H + 3) / 4);
+    hipLaunchKernelGGL(append_write_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(append_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(append_rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a);
+    return launch_status("cache_append");
+}
+
+extern "C" int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void* buf, int32_t* state,
+                                int32_t B, int32_t H, int32_t TS, int32_t D, hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "bf16_append: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(B > 0 && H > 0 && TS > 0, "bf16_append: bad shape");
+    EXKV_REQUIRE(x && buf && state, "bf16_append: null pointer");
+    hipLaunchKernelGGL(bf16_append_kernel, dim3((unsigned)((B * H + 3) / 4)), dim3(256), 0, stream,
+                       (const uint16_t*)x, sx_b, sx_h, (uint16_t*)buf, (const int32_t*)state, B, H, TS);
+    hipLaunchKernelGGL(bump_kernel, dim3(1), dim3(1), 0, stream, state, TS);
+    return launch_status("bf16_append");
+}
+
+extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,
+                                   const int32_t* rowoff, const void* raw, int64_t raw_rows, void* out,
+                                   int32_t B, int32_t T, int32_t TS, int32_t H, int32_t D, hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "decode_to_bf16: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(TS > 0 && TS % kPage == 0 && B > 0 && H > 0, "decode_to_bf16: bad shape");
+    EXKV_REQUIRE(T >= 0 && T <= TS, "decode_to_bf16: T=%d outside [0, TS=%d]", T, TS);
+    EXKV_REQUIRE(raw_rows > 0, "decode_to_bf16: empty raw pool");
+    EXKV_REQUIRE(sm && code && base && rowmask && rowoff && raw && out, "decode_to_bf16: null pointer");
+    if (T == 0) return EXKV_OK;
+    DecArgs a{CSrc{(const uint8_t*)sm, (const uint8_t*)code, (const uint8_t*)base, rowmask, rowoff,
+                   (const uint16_t*)raw, raw_rows},
+              (uint16_t*)out, B, T, TS, H};
+    const int64_t n = (int64_t)B * (TS / kPage) * H;
+    hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a);
+    return launch_status("decode_to_bf16");
+}

@@ -1,0 +1,176 @@
+"""Kernel-level API (drop-in for the reference's exactkv/kernels.py), backed by the HIP
+library: decode attention over the compressed cache, the bit-identical uncompressed
+twin, the compressed -> bf16 decoder and the page encoder.
+
+Reference signatures kept: attention_compressed(q, kc, vc, T, BLOCK_N, num_warps,
+num_stages) (kernels.py:310), attention_reference(q, k, v, T, ...) (:321),
+decode_to_bf16(c, T) (:331), encode_pages(src, strides, buf, b0, pg0, nb, npg) (:340),
+choose_split (:273), P, LOG2E. BLOCK_N / num_warps / num_stages are accepted for
+compatibility; the gfx950 kernels use one tiling (32-token chunks, 4 wavefronts), so
+the compressed and uncompressed results are identical for any value of them.
+
+Additive keywords: lens (int32 [B] device tensor of per-sequence lengths; then T is
+ignored and splits are planned over the buffer length), nsplit / split_len (explicit
+split plan), out (output tensor).
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+
+LOG2E = 1.4426950408889634
+P = 16
+D_SUPPORTED = 128
+
+
+def choose_split(B, Hkv, T, BLOCK_N, target=512):
+    """The reference planner (kernels.py:273-277), kept for API compatibility: about
+    `target` programs, split length a multiple of BLOCK_N. Returns (nsplit, split_len)."""
+    ns = max(1, min(-(-T // BLOCK_N), target // max(1, B * Hkv)))
+    split_len = -(-(-(-T // ns)) // BLOCK_N) * BLOCK_N
+    return -(-T // split_len), split_len
+
+
+def plan_splits(B, Hkv, Hq, T, target_blocks=1024, min_split=256):
+    """MI355X split plan (native): about `target_blocks` workgroups over 256 CUs, at least
+    `min_split` tokens per split, split length a multiple of 32. Returns (nsplit, split_len)."""
+    ns, sl = ctypes.c_int32(), ctypes.c_int32()
+    _lib.call("exkv_plan_splits", B, Hkv, Hq, T, target_blocks, min_split, ctypes.byref(ns), ctypes.byref(sl))
+    return ns.value, sl.value
+
+
+_WS = {}  # split partials, reused per (device, stream, rows, nsplit): kernels on one stream run in order
+
+
+def _workspace(dev, rows, ns):
+    key = (dev.index, _lib.stream(), rows, ns)
+    ws = _WS.get(key)
+    if ws is None:
+        f32 = dict(device=dev, dtype=torch.float32)
+        ws = _WS[key] = (torch.empty(rows, ns, D_SUPPORTED, **f32), torch.empty(rows, ns, **f32),
+                         torch.empty(rows, ns, **f32))
+    return ws
+
+
+def _check_q(q):
+    if q.dim() != 3 or q.shape[2] != D_SUPPORTED:
+        raise ValueError(f"q must be [B, Hq, 128] (got {tuple(q.shape)})")
+    if q.dtype != torch.bfloat16 or not q.is_contiguous() or not q.is_cuda:
+        raise ValueError("q must be a contiguous bf16 GPU tensor")
+
+
+def _cache_args(c):
+    """(seven compressed-cache arguments, TS, Hkv, B) from a CompressedKV or its buffers() dict."""
+    if isinstance(c, dict):
+        B, TS, H, D = c["shape"]
+        raw = c["raw"]
+        args = (c["sm"], c["code"], c["base"], c["rowmask"], c["rowoff"], raw)
+    else:
+        B, TS, H = c.B, c.TS, c.H
+        args = c.kernel_args()
+        raw = args[5]
+    for t, name in zip(args, ("sm", "code", "base", "rowmask", "rowoff", "raw")):
+        if not t.is_contiguous():
+            raise ValueError(f"compressed cache tensor {name} must be contiguous")
+    if raw.shape[0] < 1:
+        raise ValueError("raw pool must have at least one row")
+    ptrs = [_lib.ptr(t, what=n) for t, n in zip(args, ("sm", "code", "base", "rowmask", "rowoff", "raw"))]
+    return (*ptrs, raw.shape[0]), TS, H, B
+
+
+def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len):
+    if nsplit is not None and split_len is not None:
+        return nsplit, split_len
+    return plan_splits(B, Hkv, Hq, TS if lens is not None else T)
+
+
+def _lens_arg(lens, B):
+    if lens is None:
+        return None, 0
+    if lens.dtype != torch.int32 or not lens.is_cuda or lens.numel() < 1:
+        raise ValueError("lens must be an int32 GPU tensor")
+    stride = lens.stride(0) if lens.numel() > 1 else 0
+    if lens.numel() > 1 and lens.numel() < B:
+        raise ValueError(f"lens has {lens.numel()} entries for B={B}")
+    return _lib.ptr(lens, align=4, what="lens"), stride
+
+
+def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
+                         split_len=None, out=None):
+    """q [B, Hq, 128] bf16 contiguous; kc, vc: CompressedKV objects (or their .buffers()
+    dicts); T: valid tokens. Returns bf16 [B, Hq, 128], bit-identical to
+    attention_reference on the same contents and split plan."""
+    _check_q(q)
+    ka, TS, Hkv, Bc = _cache_args(kc)
+    va, TSv, Hv, Bv = _cache_args(vc)
+    B, Hq, D = q.shape
+    if (TSv, Hv) != (TS, Hkv) or Bc < B or Bv < B:
+        raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
+    lp, lstride = _lens_arg(lens, B)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    out = torch.empty_like(q) if out is None else out
+    _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
+              _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+    return out
+
+
+def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
+                        split_len=None, out=None):
+    """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous)."""
+    _check_q(q)
+    if k.shape != v.shape or k.dim() != 4 or k.dtype != torch.bfloat16 or not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("k and v must be contiguous bf16 [B, TS, Hkv, 128] tensors of one shape")
+    B, Hq, D = q.shape
+    TS, Hkv = k.shape[1], k.shape[2]
+    if k.shape[0] < B or k.shape[3] != D:
+        raise ValueError("k/v hold fewer sequences than q or have the wrong head dim")
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
+    lp, lstride = _lens_arg(lens, B)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    out = torch.empty_like(q) if out is None else out
+    _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
+              wl.data_ptr(), _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
+              _lib.stream())
+    return out
+
+
+def decode_to_bf16(c, T):
+    """Compressed buffers (a buffers() dict or CompressedKV) -> bf16 [B, T, H, 128],
+    through the same page decoder attention uses."""
+    ka, TS, H, B = _cache_args(c)
+    dev = (c["sm"] if isinstance(c, dict) else c.sm).device
+    out = torch.empty(B, T, H, D_SUPPORTED, dtype=torch.bfloat16, device=dev)
+    _lib.call("exkv_decode_to_bf16", *ka, _lib.ptr(out), B, int(T), TS, H, D_SUPPORTED, _lib.stream())
+    return out
+
+
+def _check_source(src, strides, nb, npg, H):
+    if src.dtype != torch.bfloat16 or not src.is_cuda:
+        raise ValueError("encode source must be a bf16 GPU tensor")
+    if src.stride(-1) != 1:
+        raise ValueError("encode source rows (head dim) must be contiguous")
+    if any(s < 0 for s in strides):
+        raise ValueError("negative source strides")
+    s_b, s_pg, s_p, s_h = strides
+    last = (nb - 1) * s_b + (npg - 1) * s_pg + (P - 1) * s_p + (H - 1) * s_h + D_SUPPORTED - 1
+    avail = src.untyped_storage().nbytes() // 2 - src.storage_offset()
+    if nb > 0 and npg > 0 and last >= avail:
+        raise ValueError(f"encode source too small: needs element {last}, has {avail}")
+
+
+def encode_pages(src, strides, buf, b0, pg0, nb, npg):
+    """Encode nb sequences x npg pages. src points at sequence b0's first page to encode;
+    strides = (seq, page, token, head) in elements. buf: dict with sm, code, base, rowmask,
+    rowoff, raw, cnt, cap, TS, H, D (optionally 'before', the counter before the call).
+    Raw rows get slots in (sequence, page, head, token) order from the counter on."""
+    H, TS, D = buf["H"], buf["TS"], buf["D"]
+    _check_source(src, strides, nb, npg, H)
+    raw = buf["raw"]
+    before = buf.get("before")
+    _lib.call("exkv_encode_pages", _lib.ptr(src, align=2, what="src"), *[int(s) for s in strides],
+              _lib.ptr(buf["sm"]), _lib.ptr(buf["code"]), _lib.ptr(buf["base"]), _lib.ptr(buf["rowmask"]),
+              _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4),
+              _lib.ptr(before, align=4) if before is not None else None, int(buf["cap"]), raw.shape[0],
+              buf["sm"].shape[0], int(b0), int(pg0), int(nb), int(npg), H, TS, D, _lib.stream())

@@ -1,0 +1,128 @@
+/* exactkv on MI355X -- C ABI of libexactkv_hip.so (gfx950).
+ *
+ * The drop-in boundary of the compressed-KV decode path. Each entry point replaces one
+ * launch site of the reference (zyfyz666/exactkv, Python + Triton); the reference file:line
+ * it stands in for is given above each declaration.
+ *
+ * Conventions
+ *   - All pointers are device pointers (HIP), except the outputs of exkv_plan_splits.
+ *   - Work is enqueued on `stream` only; nothing synchronizes, nothing allocates, so
+ *     calls can be captured in a HIP graph. The library holds no device state.
+ *   - bf16 tensors are passed as raw 16-bit patterns. Tensors are row-major with the
+ *     shapes given; "elements" strides count bf16 elements.
+ *   - Return value: 0 ok, 1 invalid argument, 2 HIP launch error; exkv_last_error()
+ *     returns the message of the last failure on the calling thread.
+ *   - Head dim is 128 and pages hold 16 tokens (the only sizes the format defines).
+ *   - Compressed cache of one layer's keys or values (reference cache.py:24-32):
+ *       sm [B, TS, H, 128] u8, code [B, TS, H, 64] u8, base [B, TS/16, H, 128] u8,
+ *       rowmask, rowoff [B, TS/16, H] i32, raw [raw_rows, 128] bf16 with
+ *       raw_rows = cap + B*H*16 (rows that do not fit | open-page tail area),
+ *       cnt / before: i32 pool counter and its value before the last encode.
+ */
+#ifndef EXACTKV_H
+#define EXACTKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/* ABI version of the library (1). */
+int exkv_abi_version(void);
+
+/* Message of the last failed call on this thread. */
+const char* exkv_last_error(void);
+
+/* Page encoder: encode nb sequences x npg pages x H heads of `src` (bf16, element strides
+ * s_b, s_pg, s_p, s_h for sequence, page, token-in-page, head; channels contiguous) into
+ * pages [pg0, pg0+npg) of sequences [b0, b0+nb) of the cache. Raw rows get pool slots
+ * *cnt + running count in (sequence, page, head, token) order; rows whose slot is >= cap
+ * are not written, and *cnt advances by the call's total (overflow = *cnt > cap).
+ * *before (may be NULL) receives the counter's value before the call.
+ * Replaces: kernels.py:340-346 encode_pages (launch of _encode_pages_kernel :233-268),
+ * byte-identical to codec.py:31-55 encode_reference. */
+int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
+                      void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
+                      int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
+                      int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
+                      int32_t D, hipStream_t stream);
+
+/* Append one token per sequence (x: [B, H, 128] bf16, row strides sx_b, sx_h) to the cache
+ * whose token count is state[0] (device): write it into the tail area; when it completes
+ * page T/16, encode that page (slots as above, *before = counter before) and open the next
+ * page (rowmask 0xFFFF, rowoff into the tail area); then state[0] += 1. Nothing is written
+ * once state[0] == TS.
+ * Replaces: cache.py:100-112 CompressedKV.append (tail write + _encode + _open_tail). */
+int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
+                      int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
+                      int32_t* state, int64_t cap, int64_t raw_rows, int32_t B, int32_t H, int32_t TS,
+                      int32_t D, hipStream_t stream);
+
+/* Append to a plain bf16 cache buf [B, TS, H, 128] at position state[0]; state[0] += 1.
+ * Replaces: cache.py:141-143 BF16KV.append. */
+int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void* buf, int32_t* state, int32_t B,
+                     int32_t H, int32_t TS, int32_t D, hipStream_t stream);
+
+/* Compressed cache -> bf16 out [B, T, H, 128] through the attention kernels' page decoder.
+ * Replaces: kernels.py:331-337 decode_to_bf16 (_dec_only_kernel :197-211). */
+int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,
+                        const int32_t* rowoff, const void* raw, int64_t raw_rows, void* out, int32_t B,
+                        int32_t T, int32_t TS, int32_t H, int32_t D, hipStream_t stream);
+
+/* Split-K GQA decode attention over compressed K and V caches, then the split merge.
+ * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
+ * ws_m, ws_l [B*Hq, nsplit] f32. Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
+ * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
+ * qk_scale = 128^-1/2 * log2(e). Bit-identical to exkv_attn_bf16 on the decoded contents.
+ * Replaces: kernels.py:310-318 attention_compressed (_split_c_kernel :142-165 and
+ * _reduce_kernel :33-43). */
+int exkv_attn_compressed(const void* q, const void* k_sm, const void* k_code, const void* k_base,
+                         const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
+                         int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
+                         const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
+                         int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, void* out, int32_t B,
+                         int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t* lens,
+                         int64_t lens_stride, int32_t nsplit, int32_t split_len, float qk_scale,
+                         hipStream_t stream);
+
+/* The same attention over plain bf16 caches k, v [B, TS, Hkv, 128].
+ * Replaces: kernels.py:321-328 attention_reference (_split_ref_kernel :168-194). */
+int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
+                   void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                   const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
+                   float qk_scale, hipStream_t stream);
+
+/* The two phases of exkv_attn_compressed / exkv_attn_bf16 separately: the split kernel
+ * (partials into ws_o, ws_m, ws_l) and the merge of `nsplit` partials per row into
+ * out [rows, 128] bf16 (rows = B*Hq).
+ * Replaces: the _split_c_kernel / _split_ref_kernel launches (kernels.py:316-317, :325-327)
+ * and kernels.py:295-299 _reduce (_reduce_kernel :33-43). */
+int exkv_attn_split_compressed(const void* q, const void* k_sm, const void* k_code, const void* k_base,
+                               const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
+                               int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
+                               const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
+                               int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, int32_t B,
+                               int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t* lens,
+                               int64_t lens_stride, int32_t nsplit, int32_t split_len, float qk_scale,
+                               hipStream_t stream);
+int exkv_attn_split_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                         const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
+                         float qk_scale, hipStream_t stream);
+int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, void* out, int64_t rows,
+                     int32_t nsplit, int32_t D, hipStream_t stream);
+
+/* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
+ * (<= 0: 1024), at least min_split tokens per split (<= 0: 256), split_len a multiple of 32.
+ * Replaces: kernels.py:273-277 choose_split. */
+int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
+                     int32_t min_split, int32_t* nsplit, int32_t* split_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXACTKV_H */

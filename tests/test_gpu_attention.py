@@ -1,0 +1,153 @@
+"""Decode attention on the GPU (reference kernels.py:142-194, :33-43; reference test
+tests/test_exactkv.py:61-78).
+
+Gates:
+  * compressed == uncompressed twin, bit for bit (same contents, same split plan);
+  * within the north-star tolerance of the oracle's fp32 attention: per element
+    |o - r| <= 1e-2 |r| + 2 bf16 ulp of the output row's largest magnitude;
+  * within the reference's own bound of 2e-2 absolute vs fp64 softmax attention.
+"""
+import numpy as np
+import pytest
+import torch
+
+import exactkv_amd as exactkv
+from exactkv_amd import kernels, synthetic
+from oracle import attention as oatt
+from tests.conftest import same_bits, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def assert_bf16_tolerance(out, ref):
+    """out: bf16 tensor; ref: float array [B, Hq, D] (fp32 oracle)."""
+    o = out.float().cpu().numpy().astype(np.float64)
+    r = ref.astype(np.float64)
+    rowmax = np.abs(r).max(-1, keepdims=True)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(rowmax, 1e-30))) - 7)
+    bound = 1e-2 * np.abs(r) + 2 * ulp
+    err = np.abs(o - r)
+    assert (err <= bound).all(), f"max excess {(err - bound).max():.3g}, max err {err.max():.3g}"
+
+
+def _encode(x):
+    B, T, H, D = x.shape
+    c = exactkv.CompressedKV(B, T, H, D, reserve=1.0)
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16)
+    return c
+
+
+def _ref_case(B, T, Hq, Hkv, seed):
+    """The reference test's data recipe (tests/test_exactkv.py:64-69), CPU seeded."""
+    g = torch.Generator().manual_seed(seed)
+    TS = -(-T // 16) * 16
+    scale = torch.exp(torch.randn(Hkv, 128, generator=g) * 0.7)
+    k = (torch.randn(B, TS, Hkv, 128, generator=g) * scale).to(torch.bfloat16)
+    v = torch.randn(B, TS, Hkv, 128, generator=g).to(torch.bfloat16)
+    k[:, ::97, :, 3] = 0.0
+    q = (torch.randn(B, Hq, 128, generator=g) * 0.3).to(torch.bfloat16)
+    return q, k, v
+
+
+SHAPES = [(1, 4096, 28, 4), (3, 1000, 32, 8), (2, 333, 32, 32), (4, 17, 16, 2), (2, 500, 64, 2), (1, 1, 8, 1)]
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv", SHAPES)
+def test_attention_bit_identical_and_accurate(B, T, Hq, Hkv):
+    _say("attention", B, T, Hq, Hkv)
+    q, k, v = _ref_case(B, T, Hq, Hkv, seed=1 + B + T)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    o_c = kernels.attention_compressed(qd, kc.buffers(), vc.buffers(), T)
+    o_r = kernels.attention_reference(qd, kd, vd, T)
+    assert same_bits(o_c, o_r)
+    for nw in (4, 8):                                  # reference kwargs accepted; same results
+        assert same_bits(kernels.attention_compressed(qd, kc, vc, T, num_warps=nw), o_c)
+    r32 = oatt.attention(u16(q), u16(k), u16(v), T, np.float32)
+    assert_bf16_tolerance(o_c, r32)
+    r64 = oatt.attention(u16(q), u16(k), u16(v), T, np.float64)
+    assert np.abs(o_c.double().cpu().numpy() - r64).max() < 2e-2
+
+
+@pytest.mark.parametrize("ns_sl", [(1, None), (None, 32), (None, 64), (None, 96)])
+def test_split_plans(ns_sl):
+    B, T, Hq, Hkv = 2, 1000, 32, 8
+    q, k, v = _ref_case(B, T, Hq, Hkv, seed=5)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    ns, sl = ns_sl
+    if sl is None:
+        sl = -(-T // 32) * 32
+    ns = -(-T // sl)
+    _say("split plan", ns, sl)
+    o_c = kernels.attention_compressed(qd, kc, vc, T, nsplit=ns, split_len=sl)
+    o_r = kernels.attention_reference(qd, kd, vd, T, nsplit=ns, split_len=sl)
+    assert same_bits(o_c, o_r)
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+
+
+def test_synthetic_keys_with_raw_rows_and_zero_groups():
+    """Config-0 style K/V (RoPE'd keys, 0.04% zeros, 0.3% raw rows) at 32q/8kv."""
+    B, T, Hq, Hkv = 2, 2048 - 7, 32, 8
+    TS = 2048
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=21, raw_row_rate=0.01)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=22, raw_row_rate=0.01)
+    q = synthetic.make_q(B, Hq, seed=23)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    assert int(kc.cnt.item()) > 0 and int(vc.cnt.item()) > 0
+    assert (kc.base >= 128).any()                       # zero-flagged groups present
+    _say("synthetic", B, T, Hq, Hkv, "raw rows", int(kc.cnt.item()), int(vc.cnt.item()))
+    o_c = kernels.attention_compressed(qd, kc, vc, T)
+    assert same_bits(o_c, kernels.attention_reference(qd, kd, vd, T))
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+
+
+def test_per_sequence_lengths():
+    B, TS, Hq, Hkv = 4, 512, 32, 8
+    lens = [512, 333, 17, 480]
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=31)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=32)
+    q = synthetic.make_q(B, Hq, seed=33)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    ld = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    _say("lens", lens)
+    o_c = kernels.attention_compressed(qd, kc, vc, 0, lens=ld)
+    assert same_bits(o_c, kernels.attention_reference(qd, kd, vd, 0, lens=ld))
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), TS, np.float32, lens=lens))
+
+
+def test_cache_with_open_tail_page():
+    """prefill_slot leaves a partial last page in the raw tail area (all rows raw)."""
+    B, T, Hq, Hkv, TS = 3, 1000, 32, 8, 1024
+    k = synthetic.make_kv(B, T, Hkv, kind="k", seed=41)
+    v = synthetic.make_kv(B, T, Hkv, kind="v", seed=42)
+    q = synthetic.make_q(B, Hq, seed=43).to(DEV)
+    kc = exactkv.CompressedKV(B, TS, Hkv, 128)
+    vc = exactkv.CompressedKV(B, TS, Hkv, 128)
+    kr, vr = exactkv.BF16KV(B, TS, Hkv, 128), exactkv.BF16KV(B, TS, Hkv, 128)
+    for b in range(B):
+        for c, x in ((kc, k), (vc, v), (kr, k), (vr, v)):
+            c.prefill_slot(b, x[b:b + 1].to(DEV).contiguous())
+    _say("open tail", B, T, TS)
+    o_c = exactkv.decode_attention(q, kc, vc)
+    o_r = exactkv.decode_attention(q, kr, vr)
+    assert same_bits(o_c, o_r)
+    assert same_bits(kernels.decode_to_bf16(kc.buffers(), T), kr.buf[:, :T])
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+
+
+def test_bad_arguments_raise():
+    q = torch.zeros(1, 8, 128, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(1, 32, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="outside"):
+        kernels.attention_reference(q, k, k, 33)
+    with pytest.raises(ValueError):
+        kernels.attention_reference(q.float(), k, k, 3)

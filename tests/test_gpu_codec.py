@@ -1,0 +1,124 @@
+"""GPU encoder and decoder vs the CPU oracle (reference codec.py:31-73; reference GPU
+test tests/test_exactkv.py:52-58, here with all six tensors byte-identical)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import exactkv_amd as exactkv
+from exactkv_amd import synthetic
+from exactkv_amd import kernels
+from oracle import codec as ocodec
+from tests.conftest import same_bits, u16
+from tests.golden import cases
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _gpu_encode(x):
+    """Encode [B,T,H,D] with the HIP encoder into fresh cache buffers (reference tests:19-26)."""
+    B, T, H, D = x.shape
+    c = exactkv.CompressedKV(B, T, H, D, reserve=1.0)
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16)
+    assert int(c.cnt.item()) <= c.cap
+    return c
+
+
+def _compare(c, ref, name):
+    for k in ("sm", "code", "base", "rowmask", "rowoff"):
+        assert np.array_equal(getattr(c, k).cpu().numpy(), ref[k]), (name, k)
+    n = int(c.cnt.item())
+    assert n == ref["raw"].shape[0], name
+    assert np.array_equal(u16(c.raw[:n]), ref["raw"]), (name, "raw")
+
+
+@pytest.mark.parametrize("name", list(cases.CASES))
+def test_encoder_bytes_equal_oracle_and_decode_exact(name):
+    x = cases.CASES[name][0]()
+    _say("encoder", name, tuple(x.shape))
+    ref = ocodec.encode(u16(x))
+    xd = x.to(DEV)
+    c = _gpu_encode(xd)
+    _compare(c, ref, name)
+    assert same_bits(kernels.decode_to_bf16(c.buffers(), x.shape[1]), xd), name
+
+
+def test_encode_reference_api_matches_golden_bytes():
+    z = np.load(os.path.join(GOLD, "codec_vectors.npz"))
+    for name, (make, stored) in cases.CASES.items():
+        if not stored:
+            continue
+        _say("encode_reference", name)
+        x = make()
+        c = exactkv.encode_reference(x)                 # CPU in, CPU out, computed on the GPU
+        for k in ("sm", "code", "base", "rowmask", "rowoff", "raw"):
+            got = c[k].numpy() if k != "raw" else u16(c[k])
+            assert np.array_equal(got, z[f"{name}/{k}"]), (name, k)
+        assert same_bits(exactkv.decode_reference(c), x), name
+        cg = exactkv.encode_reference(x.to(DEV))        # GPU in, GPU out
+        assert cg["sm"].is_cuda and same_bits(exactkv.decode_reference(cg), x.to(DEV))
+
+
+def test_encode_reference_hashed_cases():
+    import hashlib
+    h = json.load(open(os.path.join(GOLD, "codec_hashes.json")))["cases"]
+    for name, (make, stored) in cases.CASES.items():
+        if stored:
+            continue
+        _say("encode_reference hashed", name)
+        c = exactkv.encode_reference(make().to(DEV))
+        for k in ("sm", "code", "base", "rowmask", "rowoff", "raw"):
+            a = u16(c[k]) if k == "raw" else c[k].cpu().numpy()
+            assert hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest() == h[name][k]["sha256"], (name, k)
+
+
+def test_encoder_strided_source_and_offsets():
+    """Encode pages [pg0, pg0+npg) of sequences [b0, b0+nb) from a strided view."""
+    big = synthetic.make_kv(3, 96, 8, kind="k", seed=4).to(DEV)
+    src = big[:, :, ::2]                                  # heads 0, 2, 4, 6: head stride 256
+    B, T, H, D = src.shape
+    _say("strided encode", tuple(src.shape), src.stride())
+    c = exactkv.CompressedKV(4, 128, H, D, reserve=1.0)
+    st = (src.stride(0), 16 * src.stride(1), src.stride(1), src.stride(2))
+    kernels.encode_pages(src[1:], st, c._buf(), 2, 1, 2, T // 16)        # sequences 2,3 pages 1..6
+    ref = ocodec.encode(u16(src[1:].contiguous()))
+    NP = T // 16
+    assert np.array_equal(c.sm[2:4, 16:16 + T].cpu().numpy(), ref["sm"])
+    assert np.array_equal(c.code[2:4, 16:16 + T].cpu().numpy(), ref["code"])
+    assert np.array_equal(c.base[2:4, 1:1 + NP].cpu().numpy(), ref["base"])
+    assert np.array_equal(c.rowmask[2:4, 1:1 + NP].cpu().numpy(), ref["rowmask"])
+    assert np.array_equal(c.rowoff[2:4, 1:1 + NP].cpu().numpy(), ref["rowoff"])
+    assert not c.sm[:2].any() and not c.sm[2:4, :16].any()              # nothing else written
+
+
+def test_encoder_overflow_skips_rows_past_cap():
+    x = synthetic.stress_pages(1, 64, 2, seed=9).to(DEV)       # many raw rows
+    ref = ocodec.encode(u16(x))
+    n = ref["raw"].shape[0]
+    B, T, H, D = x.shape
+    c = exactkv.CompressedKV(B, T, H, D, reserve=0.0)                   # cap 64 < n
+    assert n > c.cap
+    sentinel = torch.full_like(c.raw, 7.0)
+    c.raw.copy_(sentinel)
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16)
+    assert int(c.cnt.item()) == n and int(c._before.item()) == 0
+    assert np.array_equal(u16(c.raw[: c.cap]), ref["raw"][: c.cap])
+    assert same_bits(c.raw[c.cap:], sentinel[c.cap:])                  # tail area untouched
+
+
+@pytest.mark.parametrize("T", [1, 15, 16, 17, 100, 128])
+def test_decode_partial_lengths(T):
+    x = cases.CASES["allpat_perm"][0]().to(DEV)
+    c = _gpu_encode(x)
+    _say("decode T", T)
+    assert same_bits(kernels.decode_to_bf16(c.buffers(), T), x[:, :T])

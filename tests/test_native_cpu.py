@@ -1,0 +1,72 @@
+"""CPU-side checks of the native library (no kernel launches): it loads, exports every
+entry point include/exactkv.h declares, validates arguments before touching the GPU, and
+the value-rebuild bit logic is exact on every (sign|mantissa, code, base) combination."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from exactkv_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "exactkv.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(exkv_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_header_declares_the_bound_entry_points():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.exkv_abi_version() == _lib.ABI_VERSION
+
+
+def test_argument_errors_are_reported_without_launching():
+    lib = _lib.load()
+    # head dim 64 is not a format size: rejected before any HIP call
+    rc = lib.exkv_decode_to_bf16(1, 1, 1, 1, 1, 1, 1, 1, 1, 16, 16, 1, 64, None)
+    assert rc == 1 and b"head dim" in lib.exkv_last_error()
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, 1, 1, 32, 8, 128, 5000, 4096, None, 0, 1, 4096, 0.1, None)
+    assert rc == 1 and b"outside" in lib.exkv_last_error()
+    rc = lib.exkv_encode_pages(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 1, 0, 2, 1, 4, 64, 128, None)
+    assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
+    with pytest.raises(RuntimeError, match="split_len"):
+        _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0.1, None)
+
+
+@pytest.mark.parametrize("B,Hkv,Hq,T,expect", [
+    (8, 8, 32, 8192, (16, 512)),       # 64 (seq, head) units -> 16 splits of 512
+    (1, 8, 32, 131072, (128, 1024)),
+    (1, 4, 28, 32768, (128, 256)),     # capped by min_split 256
+    (32, 8, 32, 4096, (4, 1024)),
+    (4, 2, 16, 17, (1, 32)),
+    (2, 2, 64, 1000, (4, 256)),        # G = 32: two head groups per KV head
+])
+def test_plan_splits(B, Hkv, Hq, T, expect):
+    from exactkv_amd.kernels import plan_splits
+    ns, sl = plan_splits(B, Hkv, Hq, T)
+    assert (ns, sl) == expect
+    assert sl % 32 == 0 and ns * sl >= T and (ns - 1) * sl < T
+
+
+def test_rebuild_bitmath_exhaustive(tmp_path):
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "rebuild_check"
+    subprocess.run([hipcc, "-O2", "-o", str(exe), os.path.join(ROOT, "tests", "native", "rebuild_check.cpp")],
+                   check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
+    assert r.returncode == 0, r.stdout
+    assert "0 mismatches" in r.stdout
+    assert ctypes is not None

@@ -55,6 +55,18 @@ def attention(q, k, v, T, dtype=np.float64, lens=None):
     return out
 
 
+def tolerance_excess(out, ref):
+    """North-star accuracy bound for a bf16 attention output against a float reference:
+    per element |out - ref| <= 1e-2 |ref| + 2 bf16 ulp of the largest |ref| in the output
+    row (the row's scale: bf16 rounding alone can cost half an ulp of each element).
+    Returns max(|out - ref| - bound); the bound holds when it is <= 0."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    rowmax = np.abs(r).max(-1, keepdims=True)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(rowmax, 1e-30))) - 7)
+    return float((np.abs(o - r) - (1e-2 * np.abs(r) + 2 * ulp)).max())
+
+
 def choose_split(B, Hkv, T, BLOCK_N, target=512):
     """Reference planner (kernels.py:273-277): about `target` programs in total, split
     lengths a multiple of BLOCK_N. Returns (number of splits, split length)."""

@@ -4,17 +4,21 @@ Each case maps to (make() -> bf16 CPU tensor [B, T, H, D], store_bytes). Small c
 store their bytes in codec_vectors.npz; large ones store sha256 digests and are
 regenerated here from fixed seeds (torch CPU generator / explicit construction).
 """
+import math
+
+import numpy as np
 import torch
 
-from exactkv_amd.synthetic import all_bf16_patterns, make_kv, stress_pages
+from exactkv_amd.synthetic import _bf16_bits, all_bf16_patterns, make_kv, stress_pages
 
 
 def _mixed():
-    # the reference test's mixed recipe (tests/test_exactkv.py:33-41) on CPU seeds
-    g = torch.Generator().manual_seed(0)
-    scale = torch.exp(torch.randn(4, 128, generator=g))
+    # the reference test's mixed recipe (tests/test_exactkv.py:33-41) on a numpy stream
+    rng = np.random.Generator(np.random.PCG64(0))
+    scale = np.array([math.exp(z) for z in rng.standard_normal(4 * 128).tolist()], np.float32).reshape(4, 128)
     scale[0, 5] = 300.0
-    x = (torch.randn(2, 512, 4, 128, generator=g) * scale).to(torch.bfloat16)
+    xf = rng.standard_normal((2, 512, 4, 128), dtype=np.float32) * scale
+    x = torch.from_numpy(_bf16_bits(xf).astype(np.int16)).view(torch.bfloat16)
     x[0, 7, 1, 3] = 0.0
     x[1, 9, 2, 5] = -0.0
     x[1, 100, 2, :] = 1e-30

@@ -275,3 +275,18 @@ def test_cache_model_append_growth_stays_exact():
         if t % 13 == 0 or t == TS - T0 - 1:
             assert np.array_equal(codec.decode(m.buffers(), m.T), ref[:, : m.T]), t
     assert m.grows > 0
+
+
+def test_tolerance_bound_rejects_plausible_mistakes():
+    """The accuracy gate used on the GPU output must fail for a dropped token, a wrong head
+    and a missing bf16 rounding of p is within it."""
+    B, T, Hq, Hkv = 1, 300, 8, 2
+    q, k, v = _rand_case(B, T, Hq, Hkv, 17)
+    ref = oatt.attention(u16(q), u16(k), u16(v), T, np.float32)
+    model = oatt.split_attention(u16(q), u16(k), u16(v), T, split_len=64)
+    out = oatt.bf16_to_f32(oatt.f32_to_bf16(model))
+    assert oatt.tolerance_excess(out, ref) <= 0
+    dropped = oatt.attention(u16(q), u16(k)[:, 1:], u16(v)[:, 1:], T - 1, np.float32)
+    assert oatt.tolerance_excess(dropped, ref) > 0
+    swapped = ref[:, ::-1]
+    assert oatt.tolerance_excess(swapped, ref) > 0

@@ -116,7 +116,12 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--target-blocks", type=int, default=None)
+    ap.add_argument("--profile", action="store_true",
+                    help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
+                         "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
+    if a.profile:
+        a.copies = 1
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
               "(the decode path shards by KV head or sequence with no exchange; see DESIGN.md)", file=sys.stderr)
@@ -148,6 +153,9 @@ def main():
     print("[bench] caches encoded", file=sys.stderr, flush=True)
     ns, sl = kernels.plan_splits(B, Hkv, Hq, T, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
     out = torch.empty_like(q)
+    if a.profile:
+        profile_run(kernels, q, kcs[0], vcs[0], kbs[0], vbs[0], T, ns, sl, out)
+        return
     o_c = kernels.attention_compressed(q, kcs[0], vcs[0], T, nsplit=ns, split_len=sl)
     o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl)
     identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
@@ -192,6 +200,26 @@ def main():
         res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, min(a.cpu_seqs, B))
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
+
+
+def profile_run(kernels, q, kc, vc, kb, vb, T, ns, sl, out):
+    """Launch sequence for hardware-counter runs: the calibration copy, then 5 launches each
+    of the compressed split kernel, the bf16 split kernel and the full compressed call."""
+    import torch
+    n = 64 << 20                                             # 64 Mi floats: 256 MiB read + 256 MiB written
+    src = torch.ones(n, dtype=torch.float32, device=q.device)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        split_only(kernels, q, kc, vc, T, ns, sl, True)
+    for _ in range(5):
+        split_only(kernels, q, kb, vb, T, ns, sl, False)
+    for _ in range(5):
+        kernels.attention_compressed(q, kc, vc, T, nsplit=ns, split_len=sl, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_run": True, "copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
+                      "nsplit": ns, "split_len": sl}), flush=True)
 
 
 def split_only(kernels, q, kc, vc, T, ns, sl, compressed):

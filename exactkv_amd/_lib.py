@@ -7,7 +7,8 @@ library is missing or a call fails.
 import ctypes
 import os
 
-_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
+# EXACTKV_LIB overrides the path of the library to load (default: the in-tree build)
+_PATH = os.environ.get("EXACTKV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
 ABI_VERSION = 1
 
 _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
@@ -20,9 +21,9 @@ SIGNATURES = {
                           _i32, _p],
     "exkv_bf16_append": [_p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _p],
     "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
-    "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p,
+    "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
                              _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
-    "exkv_attn_bf16": [_p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
+    "exkv_attn_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
                        _f32, _p],
     "exkv_attn_split_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p,
                                    _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],

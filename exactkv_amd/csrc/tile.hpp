@@ -55,16 +55,19 @@ __device__ inline void rebuild_page_impl(const PageBytes& pb, uint32_t out[16]) 
     for (int i = 0; i < 4; ++i) {
         const uint32_t cl = C[i] & 0x0F0F0F0Fu;
         const uint32_t ch = (C[i] >> 4) & 0x0F0F0F0Fu;
-        rebuild4<Z>(S[i], cl, BL[i] & 0x7F7F7F7Fu, BL[i] & 0x80808080u, out[2 * i], out[2 * i + 1]);
-        rebuild4<Z>(SH[i], ch, BH[i] & 0x7F7F7F7Fu, BH[i] & 0x80808080u, out[8 + 2 * i], out[8 + 2 * i + 1]);
+        if (Z) {
+            rebuild4<true>(S[i], cl, BL[i] & 0x7F7F7F7Fu, BL[i] & 0x80808080u, out[2 * i], out[2 * i + 1]);
+            rebuild4<true>(SH[i], ch, BH[i] & 0x7F7F7F7Fu, BH[i] & 0x80808080u, out[8 + 2 * i], out[8 + 2 * i + 1]);
+        } else {                               // no zero flag in the page: base bytes are < 128
+            rebuild4<false>(S[i], cl, BL[i], 0u, out[2 * i], out[2 * i + 1]);
+            rebuild4<false>(SH[i], ch, BH[i], 0u, out[8 + 2 * i], out[8 + 2 * i + 1]);
+        }
     }
 }
 
-// Rebuild the lane's 32 values, then splice raw rows (reference kernels.py:106-128):
-// a raw row's slot is rowoff + popcount(rowmask & ((1 << r) - 1)). The slot is clamped
-// to the pool so that a page whose raw rows did not fit (the pool counter passed its
-// capacity, which the host repairs by growing and re-encoding) cannot read out of bounds.
-__device__ inline void rebuild_page(const CSrc& c, const PageBytes& pb, int r, int g, uint32_t out[16]) {
+// Rebuild the lane's 32 values (the zero-group fix-up only when a group of this page
+// carries the zero flag, decided for the whole wavefront).
+__device__ inline void rebuild_values(const PageBytes& pb, uint32_t out[16]) {
     const uint32_t fl = (pb.b_lo.x | pb.b_lo.y | pb.b_lo.z | pb.b_lo.w | pb.b_hi.x | pb.b_hi.y |
                          pb.b_hi.z | pb.b_hi.w) & 0x80808080u;
     if (__ballot(fl != 0) != 0) {             // any zero-flagged group in this page
@@ -72,18 +75,33 @@ __device__ inline void rebuild_page(const CSrc& c, const PageBytes& pb, int r, i
     } else {
         rebuild_page_impl<false>(pb, out);
     }
+}
+
+// Slot of token r's raw row: rowoff + popcount(rowmask & ((1 << r) - 1)) (reference
+// kernels.py:119-123), clamped to the pool so that a page whose raw rows did not fit
+// (the pool counter passed its capacity, which the host repairs by growing and
+// re-encoding) cannot read out of bounds.
+__device__ inline int64_t raw_slot(uint32_t rmask, int32_t roff, int r, int64_t raw_rows) {
+    int64_t slot = (int64_t)roff + popc32(rmask & ((1u << r) - 1u));
+    return slot < 0 ? 0 : (slot >= raw_rows ? raw_rows - 1 : slot);
+}
+
+// The lane's 32 values of a raw row (channels 16g.. and 64+16g..).
+__device__ inline void load_raw_values(const uint16_t* raw, int64_t slot, int g, uint32_t out[16]) {
+    const uint8_t* rp = reinterpret_cast<const uint8_t*>(raw + slot * 128) + 32 * g;
+    const uint4 a0 = ld16(rp), a1 = ld16(rp + 16), h0 = ld16(rp + 128), h1 = ld16(rp + 144);
+    out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
+    out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
+    out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;
+    out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
+}
+
+// Rebuild, then splice raw rows straight from the pool (reference kernels.py:106-128).
+__device__ inline void rebuild_page(const CSrc& c, const PageBytes& pb, int r, int g, uint32_t out[16]) {
+    rebuild_values(pb, out);
     if (pb.rmask != 0) {
         const uint32_t m = (uint32_t)pb.rmask;
-        if ((m >> r) & 1u) {
-            int64_t slot = (int64_t)pb.roff + popc32(m & ((1u << r) - 1u));
-            slot = slot < 0 ? 0 : (slot >= c.raw_rows ? c.raw_rows - 1 : slot);
-            const uint8_t* rp = reinterpret_cast<const uint8_t*>(c.raw + slot * 128) + 32 * g;
-            const uint4 a0 = ld16(rp), a1 = ld16(rp + 16), h0 = ld16(rp + 128), h1 = ld16(rp + 144);
-            out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
-            out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
-            out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;
-            out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
-        }
+        if ((m >> r) & 1u) load_raw_values(c.raw, raw_slot(m, pb.roff, r, c.raw_rows), g, out);
     }
 }
 

@@ -6,7 +6,7 @@ Reference signatures kept: attention_compressed(q, kc, vc, T, BLOCK_N, num_warps
 num_stages) (kernels.py:310), attention_reference(q, k, v, T, ...) (:321),
 decode_to_bf16(c, T) (:331), encode_pages(src, strides, buf, b0, pg0, nb, npg) (:340),
 choose_split (:273), P, LOG2E. BLOCK_N / num_warps / num_stages are accepted for
-compatibility; the gfx950 kernels use one tiling (32-token chunks, 4 wavefronts), so
+compatibility; the gfx950 kernels use one tiling (16-token pages, 8 wavefronts), so
 the compressed and uncompressed results are identical for any value of them.
 
 Additive keywords: lens (int32 [B] device tensor of per-sequence lengths; then T is
@@ -14,6 +14,7 @@ ignored and splits are planned over the buffer length), nsplit / split_len (expl
 split plan), out (output tensor).
 """
 import ctypes
+import math
 
 import torch
 
@@ -32,8 +33,8 @@ def choose_split(B, Hkv, T, BLOCK_N, target=512):
     return -(-T // split_len), split_len
 
 
-def plan_splits(B, Hkv, Hq, T, target_blocks=1024, min_split=256):
-    """MI355X split plan (native): about `target_blocks` workgroups over 256 CUs, at least
+def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=256):
+    """MI355X split plan (native): about `target_blocks` workgroups (one per CU), at least
     `min_split` tokens per split, split length a multiple of 32. Returns (nsplit, split_len)."""
     ns, sl = ctypes.c_int32(), ctypes.c_int32()
     _lib.call("exkv_plan_splits", B, Hkv, Hq, T, target_blocks, min_split, ctypes.byref(ns), ctypes.byref(sl))
@@ -41,6 +42,7 @@ def plan_splits(B, Hkv, Hq, T, target_blocks=1024, min_split=256):
 
 
 _WS = {}  # split partials, reused per (device, stream, rows, nsplit): kernels on one stream run in order
+_CNT = {}  # merge arrival counters per (device, stream, units): zero between calls
 
 
 def _workspace(dev, rows, ns):
@@ -51,6 +53,23 @@ def _workspace(dev, rows, ns):
         ws = _WS[key] = (torch.empty(rows, ns, D_SUPPORTED, **f32), torch.empty(rows, ns, **f32),
                          torch.empty(rows, ns, **f32))
     return ws
+
+
+def merge_units(B, Hkv, Hq):
+    """Workgroup units of the split kernel: sequences x KV-head blocks of gcd(Hkv, 8) x
+    groups of 16 query heads per KV head."""
+    return B * (Hkv // math.gcd(Hkv, 8)) * (-(-(Hq // Hkv) // 16))
+
+
+FUSED_MERGE_MAX_SPLITS = 4   # up to this many splits the split kernel's last workgroup merges
+
+
+def _counters(dev, units):
+    key = (dev.index, _lib.stream(), units)
+    c = _CNT.get(key)
+    if c is None:
+        c = _CNT[key] = torch.zeros(units, dtype=torch.int32, device=dev)
+    return c
 
 
 def _check_q(q):
@@ -110,9 +129,11 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    cnt = _counters(q.device, merge_units(B, Hkv, Hq)) if ns <= FUSED_MERGE_MAX_SPLITS else None
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
-              _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+              cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
+              _lib.stream())
     return out
 
 
@@ -129,10 +150,11 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    cnt = _counters(q.device, merge_units(B, Hkv, Hq)) if ns <= FUSED_MERGE_MAX_SPLITS else None
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
-              wl.data_ptr(), _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
-              _lib.stream())
+              wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl,
+              D ** -0.5 * LOG2E, _lib.stream())
     return out
 
 

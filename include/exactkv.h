@@ -74,7 +74,11 @@ int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, cons
 
 /* Split-K GQA decode attention over compressed K and V caches, then the split merge.
  * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
- * ws_m, ws_l [B*Hq, nsplit] f32. Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
+ * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: B*(Hkv/gcd(Hkv,8))*ceil(Hq/Hkv/16) i32 arrival
+ * counters, all zero before the first call (each call leaves them zero); with ws_cnt the
+ * merge runs inside the split kernel (its last workgroup per unit), with ws_cnt == NULL as
+ * a second kernel (same bits). Calls that share a workspace must not overlap.
+ * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
  * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
  * qk_scale = 128^-1/2 * log2(e). Bit-identical to exkv_attn_bf16 on the decoded contents.
  * Replaces: kernels.py:310-318 attention_compressed (_split_c_kernel :142-165 and
@@ -83,15 +87,15 @@ int exkv_attn_compressed(const void* q, const void* k_sm, const void* k_code, co
                          const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
                          int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
                          const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
-                         int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, void* out, int32_t B,
-                         int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t* lens,
-                         int64_t lens_stride, int32_t nsplit, int32_t split_len, float qk_scale,
-                         hipStream_t stream);
+                         int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, int32_t* ws_cnt, void* out,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                         const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
+                         float qk_scale, hipStream_t stream);
 
 /* The same attention over plain bf16 caches k, v [B, TS, Hkv, 128].
  * Replaces: kernels.py:321-328 attention_reference (_split_ref_kernel :168-194). */
 int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
-                   void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                   int32_t* ws_cnt, void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                    const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
                    float qk_scale, hipStream_t stream);
 
@@ -116,7 +120,7 @@ int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, vo
                      int32_t nsplit, int32_t D, hipStream_t stream);
 
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
- * (<= 0: 1024), at least min_split tokens per split (<= 0: 256), split_len a multiple of 32.
+ * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 256), split_len a multiple of 32.
  * Replaces: kernels.py:273-277 choose_split. */
 int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);

@@ -36,19 +36,20 @@ def test_argument_errors_are_reported_without_launching():
     # head dim 64 is not a format size: rejected before any HIP call
     rc = lib.exkv_decode_to_bf16(1, 1, 1, 1, 1, 1, 1, 1, 1, 16, 16, 1, 64, None)
     assert rc == 1 and b"head dim" in lib.exkv_last_error()
-    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, 1, 1, 32, 8, 128, 5000, 4096, None, 0, 1, 4096, 0.1, None)
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 5000, 4096, None, 0, 1, 4096, 0.1, None)
     assert rc == 1 and b"outside" in lib.exkv_last_error()
     rc = lib.exkv_encode_pages(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 1, 0, 2, 1, 4, 64, 128, None)
     assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
     with pytest.raises(RuntimeError, match="split_len"):
-        _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0.1, None)
+        _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0.1, None)
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,expect", [
-    (8, 8, 32, 8192, (16, 512)),       # 64 (seq, head) units -> 16 splits of 512
-    (1, 8, 32, 131072, (128, 1024)),
-    (1, 4, 28, 32768, (128, 256)),     # capped by min_split 256
-    (32, 8, 32, 4096, (4, 1024)),
+    (8, 8, 32, 8192, (32, 256)),       # a workgroup covers all 8 KV heads: 8 units x 32 splits = 256
+    (1, 8, 32, 131072, (256, 512)),
+    (1, 4, 28, 32768, (128, 256)),     # 4 KV heads per workgroup; capped by min_split 256
+    (32, 8, 32, 4096, (8, 512)),
+    (1, 4, 28, 8000, (32, 256)),
     (4, 2, 16, 17, (1, 32)),
     (2, 2, 64, 1000, (4, 256)),        # G = 32: two head groups per KV head
 ])

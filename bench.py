@@ -77,6 +77,36 @@ def time_loop(fn, n, warmup, copies):
     return e0.elapsed_time(e1) / n
 
 
+def time_graph(fn, n, warmup, copies, per_graph=20):
+    """Average ms per call of fn(i) with the calls captured in a HIP graph (per_graph calls
+    rotating over `copies` inputs) and the graph replayed until n calls ran: the launch
+    path of a captured decode step, with no Python work between kernels. Workspaces are
+    allocated by eager calls on the capture stream beforehand; timed with HIP events on
+    the stream the graph is launched on."""
+    import torch
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        for i in range(max(warmup, copies)):
+            fn(i % copies)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for i in range(per_graph):
+            fn(i % copies)
+    torch.cuda.synchronize()
+    reps = max(1, -(-n // per_graph))
+    with torch.cuda.stream(cs):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cs)
+        for _ in range(reps):
+            g.replay()
+        e1.record(cs)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * per_graph)
+
+
 def cpu_baseline(kc, vc, q, B, T, nseq):
     """The oracle (restated reference codec decode + fp32 GQA attention, numpy, 1 thread) on
     the first `nseq` sequences; reported as microseconds for the full B-sequence call."""
@@ -160,14 +190,19 @@ def main():
     o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl)
     identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
 
-    ms_c = time_loop(lambda i: kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl,
-                                                            out=out), a.steps, a.warmup, a.copies)
-    ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl,
-                                                           out=out), a.steps, a.warmup, a.copies)
+    def full_c(i):
+        kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl, out=out)
+
+    def full_b(i):
+        kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out)
+
+    ms_c = time_loop(full_c, a.steps, a.warmup, a.copies)
+    ms_b = time_loop(full_b, a.steps, a.warmup, a.copies)
     ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True), a.steps, a.warmup,
                          a.copies)
-    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False), a.steps, a.warmup,
-                           a.copies)
+    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False), a.steps,
+                           a.warmup, a.copies)
+    ms_c_graph = time_graph(full_c, a.steps, a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
 
     alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv)
@@ -187,6 +222,8 @@ def main():
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
                      "kernel_us": round(ms_split * 1e3, 2)},
+        "timing": "HIP events around back-to-back calls on one stream",
+        "graph_replay_us": round(ms_c_graph * 1e3, 2),
         "bf16_twin_us": round(ms_b * 1e3, 2),
         "bf16_split_us": round(ms_split_b * 1e3, 2),
         "bf16_split_GBps": round(alg_b / (ms_split_b * 1e-3) / 1e9, 1),

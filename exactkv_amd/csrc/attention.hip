@@ -44,22 +44,58 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kDmaPerPage = 8;        // direct-to-LDS loads per page, both kernels
+constexpr int kFusedMaxSplits = 4;   // up to this many splits the split kernel merges in its tail
+constexpr int kDmaPerPage[2] = {8, 7}; // direct-to-LDS loads per page: bf16, compressed
 
 // compressed page stage (bytes): K sm 16x128 | K code 16x64 | V sm | V code | K base,
-// V base (128 each) | meta (K rowmask, K rowoff, V rowmask, V rowoff)
-constexpr int CS_KSM = 0, CS_KCODE = 2048, CS_VSM = 3072, CS_VCODE = 5120, CS_BASE = 6144,
-              CS_META = 6400, CS_BYTES = 6416;
+// V base (128 each); rowmask/rowoff come through the scalar cache instead
+constexpr int CS_KSM = 0, CS_KCODE = 2048, CS_VSM = 3072, CS_VCODE = 5120, CS_BASE = 6144, CS_BYTES = 6400;
 // bf16 page stage: K rows 16x256 | V rows 16x256
 constexpr int BS_K = 0, BS_V = 4096, BS_BYTES = 8192;
 
+// Raw rows travel with their page through the DMA ring when a page (K and V together)
+// has at most kRawRing of them: one more load per page into the wave's raw slot of the
+// page's parity. Pages with more fall back to direct loads.
+constexpr int kRawRing = 2;
+constexpr int kRawSlot = kRawRing * 256;
+
+// Per wavefront: nst page stages, then (compressed) two raw slots.
 template <bool COMP>
 struct Ring {
     static constexpr int stage = COMP ? CS_BYTES : BS_BYTES;
     static constexpr int nst = COMP ? 3 : 2;
     static constexpr int vtile = COMP ? 0 : BS_V;    // offset of the bf16 V tile in a stage
-    static constexpr int bytes = kWaves * nst * stage;
+    static constexpr int raw = COMP ? 2 * kRawSlot : 0;
+    static constexpr int per_wave = nst * stage + raw;
+    static constexpr int bytes = kWaves * per_wave;
 };
+
+// A wave-uniform 64-bit value the compiler cannot trace back to the kernel arguments: a
+// per-lane select between two such values stays a v_cndmask instead of becoming a
+// per-lane load of the chosen pointer from the argument block (and its wait for all loads).
+__device__ inline uint64_t opaque_u64(uint64_t x) {
+    asm("" : "+s"(x));
+    return x;
+}
+struct PairSrc {              // K address of one array and V minus K: per-lane selects add
+    uint64_t k, d;            // (cond ? d : 0), which cannot become a load of either pointer
+    __device__ uint64_t pick(bool v) const { return k + (v ? d : 0ull); }
+};
+__device__ inline PairSrc pair_src(uint64_t k, uint64_t v) {
+    const uint64_t ko = opaque_u64(k);
+    return PairSrc{ko, opaque_u64(v) - ko};
+}
+
+// rowmask / rowoff of one page of the K and V caches (wave-uniform)
+struct PageMeta {
+    uint32_t mk, mv;
+    int32_t ok, ov;
+};
+__device__ inline int raw_rows_of(const PageMeta& m) { return __builtin_popcount(m.mk) + __builtin_popcount(m.mv); }
+__device__ inline bool raw_in_ring(const PageMeta& m) {
+    const int n = raw_rows_of(m);
+    return n > 0 && n <= kRawRing;
+}
 
 struct AttnArgs {
     const uint16_t* q;        // [B, Hq, 128] bf16
@@ -79,38 +115,77 @@ struct AttnArgs {
 };
 
 // ---- split merge (kernels.py:33-43): M = max_s m_s, w_s = 2^(m_s - M),
-// out = sum_s o_s w_s / sum_s l_s w_s. Shared by the fused merge and attn_reduce_kernel so
-// both produce the same bits.
+// out = sum_s o_s w_s / sum_s l_s w_s, one wavefront per (sequence, query head) row with
+// lane = channel pair. Shared by the fused merge and attn_reduce_kernel so both produce
+// the same bits: the sums run over s in order with explicit fmas.
 __device__ inline float fast_exp2(float x);
-__device__ inline float split_max(const float* m, int ns) {
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, m[s]);
-    return M;
+__device__ inline float wave_max(float x) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) x = fmaxf(x, __shfl_xor(x, d));
+    return x;
 }
-__device__ inline uint32_t merge_pair(const float* po, const float* m, const float* l, int ns, float M, int dp) {
-    float n0 = 0.f, n1 = 0.f, den = 0.f;
-    int s = 0;
-    for (; s + 8 <= ns; s += 8) {                      // 8 splits' loads in flight at once
-        float2 o[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = reinterpret_cast<const float2*>(po + (int64_t)(s + i) * kD)[dp];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float w = fast_exp2(m[s + i] - M);
-            n0 += o[i].x * w;
-            n1 += o[i].y * w;
-            den += l[s + i] * w;
-        }
-    }
-    for (; s < ns; ++s) {
-        const float w = fast_exp2(m[s] - M);
-        const float2 o = reinterpret_cast<const float2*>(po + (int64_t)s * kD)[dp];
-        n0 += o.x * w;
-        n1 += o.y * w;
-        den += l[s] * w;
-    }
-    const __bf16 r0 = (__bf16)(n0 / den), r1 = (__bf16)(n1 / den);
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+    const __bf16 r0 = (__bf16)a, r1 = (__bf16)b;
     return (uint32_t)__builtin_bit_cast(uint16_t, r0) | ((uint32_t)__builtin_bit_cast(uint16_t, r1) << 16);
+}
+// Accumulate splits [c, c + n) (n <= 32): o loads all in flight together; w and l of split
+// c + i sit in lane i of ws / ls.
+__device__ __attribute__((always_inline)) inline void merge_chunk(const float2* po2, int c, int n, float ws, float ls, int lane, float& n0,
+                                   float& n1, float& den) {
+    float2 o[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        if (i < n) o[i] = po2[(int64_t)(c + i) * (kD / 2) + lane];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        if (i < n) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), i));
+            const float lv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), i));
+            n0 = __builtin_fmaf(o[i].x, w, n0);
+            n1 = __builtin_fmaf(o[i].y, w, n1);
+            den = __builtin_fmaf(lv, w, den);
+        }
+}
+// ns <= N splits in one round trip: m, l and o loads issued together.
+template <int N>
+__device__ __attribute__((always_inline)) inline uint32_t merge_direct(const float* po, const float* m,
+                                                                        const float* l, int ns, int lane) {
+    const float2* po2 = reinterpret_cast<const float2*>(po);
+    const float mv = lane < ns ? m[lane] : -INFINITY;
+    const float lv = lane < ns ? l[lane] : 0.f;
+    float2 o[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (i < ns) o[i] = po2[(int64_t)i * (kD / 2) + lane];
+    const float M = wave_max(mv);
+    const float ws = fast_exp2(mv - M);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (i < ns) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), i));
+            const float li = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), i));
+            n0 = __builtin_fmaf(o[i].x, w, n0);
+            n1 = __builtin_fmaf(o[i].y, w, n1);
+            den = __builtin_fmaf(li, w, den);
+        }
+    return pack_bf16x2(n0 / den, n1 / den);
+}
+__device__ __attribute__((always_inline)) inline uint32_t merge_row(const float* po, const float* m, const float* l,
+                                                                     int ns, int lane) {
+    if (ns <= 32) return merge_direct<32>(po, m, l, ns, lane);
+    const float2* po2 = reinterpret_cast<const float2*>(po);
+    float mm = -INFINITY;
+    for (int s = lane; s < ns; s += 64) mm = fmaxf(mm, m[s]);
+    const float M = wave_max(mm);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+    for (int c = 0; c < ns; c += 32) {
+        const int n = ns - c < 32 ? ns - c : 32;
+        const float ws = lane < n ? fast_exp2(m[c + lane] - M) : 0.f;
+        const float ls = lane < n ? l[c + lane] : 0.f;
+        merge_chunk(po2, c, n, ws, ls, lane, n0, n1, den);
+    }
+    return pack_bf16x2(n0 / den, n1 / den);
 }
 
 __device__ inline bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -127,11 +202,8 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline uint32_t lds_addr(const uint8_t* p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const EXKV_LDS uint8_t*)p);
 }
-__device__ inline void dma16(const void* g, uint8_t* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
-}
-__device__ inline void dma4(const void* g, uint8_t* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+__device__ inline void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
 
 // Mark registers as defined here (an empty asm that reads and writes them): the compiler
@@ -141,6 +213,27 @@ template <int N>
 __device__ inline void settle(uint32_t (&v)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+
+// Load of a wave-uniform int32 through the constant address space (an s_load_dword).
+__device__ inline int32_t const_ld(const int32_t* p) {
+    return *(const __attribute__((address_space(4))) int32_t*)p;
+}
+
+// Reductions over the 4 lane groups holding one head (lanes l, l^16, l^32, l^48) with the
+// gfx950 row-swap permutes: with both operands = x, v_permlane16_swap returns x's even and
+// odd 16-lane rows side by side (likewise v_permlane32_swap for the two halves).
+__device__ inline float group_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ inline float group_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
 }
 
 // Wait until at most n vector-memory loads of this wavefront are in flight, and keep the
@@ -184,9 +277,21 @@ __device__ inline DmaLane dma_lane_offsets(int lane, int64_t rs) {
 // Issue one page's kDmaPerPage loads into stage st. row0: row index of the page's token 0
 // ((b*TS + 16*pg)*Hkv + hk); page: its page index.
 template <bool COMP>
-__device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row0, int64_t page, uint8_t* st,
-                                int lane) {
+__device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row0, int64_t page, uint32_t st,
+                                int lane, const PageMeta& m, uint32_t raw_st, const PairSrc& basep,
+                                const PairSrc& rawp, const PairSrc& rawn) {
     if constexpr (COMP) {
+        // raw rows of the page (K rows in token order, then V rows): entry e = lane / 16 of
+        // at most kRawRing, 16 bytes per lane; pool index = rowoff + rank of the row
+        if (raw_in_ring(m)) {
+            const int nk = __builtin_popcount(m.mk), n = nk + __builtin_popcount(m.mv), e = lane >> 4;
+            const bool isv = e >= nk;
+            int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
+            const int64_t rows = (int64_t)rawn.pick(isv);
+            idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+            const uint64_t rb = rawp.pick(isv);
+            if (lane < 16 * n) dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
+        }
         const uint8_t* ksm = a.k.sm + row0 * 128;
         const uint8_t* vsm = a.v.sm + row0 * 128;
         dma16(ksm + o.sm0, st + CS_KSM);
@@ -195,13 +300,9 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
         dma16(vsm + o.sm1, st + CS_VSM + 1024);
         dma16(a.k.code + row0 * 64 + o.code, st + CS_KCODE);
         dma16(a.v.code + row0 * 64 + o.code, st + CS_VCODE);
-        // base rows (lanes 0-7 K, 8-15 V) and meta (lanes 0-3: K rowmask, K rowoff, V rowmask,
-        // V rowoff): addresses picked with bit-test selects of values already in registers
-        const uint8_t* bsrc = ((lane & 8) ? a.v.base : a.k.base) + page * 128 + o.base;
-        if (lane < 16) dma16(bsrc, st + CS_BASE);
-        const int32_t* mk = (lane & 1) ? a.k.rowoff : a.k.rowmask;
-        const int32_t* mv = (lane & 1) ? a.v.rowoff : a.v.rowmask;
-        if (lane < 4) dma4(((lane & 2) ? mv : mk) + page, st + CS_META);
+        // base rows: lanes 0-7 K, 8-15 V
+        const uint64_t bsrc = basep.pick((lane & 8) != 0) + (uint64_t)page * 128 + o.base;
+        if (lane < 16) dma16((const void*)(uintptr_t)bsrc, st + CS_BASE);
     } else {
         const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.kb) + row0 * 256;
         const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.vb) + row0 * 256;
@@ -213,37 +314,91 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
     }
 }
 
-// ---- rebuild K or V of the staged page (lane = token r, channel group g)
+// ---- per-lane LDS offsets within a stage (fixed for the kernel). With the stage base in
+// an SGPR every LDS access is one v_add plus an immediate offset; accesses whose offsets
+// differ by a constant share one register.
+struct LdsLane {
+    uint32_t sml, smh, code, base;    // compressed: sm units g and 4+g of row r, code, base
+    uint32_t tw;                      // V tile row r: units 2g (+16: 2g+1, +128: 8+2g, +144: 9+2g)
+    uint32_t tr[4];                   // transpose reads of channel blocks nb (+128: nb + 4)
+    uint32_t bk[4];                   // bf16 K row r: units 2g, 2g+1, 8+2g, 9+2g
+};
 
-__device__ inline void stage_bytes(const uint8_t* st, int sm_off, int code_off, int base_off, int r, int g,
-                                   PageBytes& pb) {
-    const uint8_t* smr = st + sm_off + r * 128;
-    pb.sm_lo = ld16(smr + 16 * (g ^ (r & 7)));
-    pb.sm_hi = ld16(smr + 16 * ((4 + g) ^ (r & 7)));
-    pb.code = ld16(st + code_off + r * 64 + 16 * (g ^ ((r >> 1) & 3)));
-    pb.b_lo = ld16(st + base_off + 16 * g);
-    pb.b_hi = ld16(st + base_off + 64 + 16 * g);
-}
-
-__device__ inline void stage_bf16_k(const uint8_t* st, int r, int g, uint32_t out[16]) {
-    const uint8_t* rp = st + BS_K + r * 256;
+__device__ inline LdsLane lds_lane_offsets(int r, int g) {
+    LdsLane o;
+    o.sml = (uint32_t)(r * 128 + 16 * (g ^ (r & 7)));
+    o.smh = (uint32_t)(r * 128 + 16 * ((4 + g) ^ (r & 7)));
+    o.code = (uint32_t)(r * 64 + 16 * (g ^ ((r >> 1) & 3)));
+    o.base = (uint32_t)(16 * g);
+    // V tile / staged bf16 V: row r's logical unit u sits at physical unit u ^ ((r & 3) << 1);
+    // the XOR only touches bits 1-2 of u, so units 2g+1, 8+2g, 9+2g follow at +16, +128, +144
+    o.tw = (uint32_t)(r * 256 + 16 * ((2 * g) ^ ((r & 3) << 1)));
+    // transpose read: lane supplies row trow = 4g + r/4, 8-byte half r & 1 of unit
+    // u = 2nb + ((r & 3) >> 1), i.e. physical 2(nb ^ (trow & 3)) + ((r & 3) >> 1) for nb < 4
+    const int trow = 4 * g + (r >> 2), xq = trow & 3, b1 = (r & 3) >> 1;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) o.tr[nb] = (uint32_t)(trow * 256 + 8 * (r & 1) + 16 * (2 * (nb ^ xq) + b1));
+    // bf16 K rows: unit u at u ^ (r & 7)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int u = (j < 2 ? 2 * g : 8 + 2 * g) + (j & 1);
-        const uint4 v = ld16(rp + 16 * (u ^ (r & 7)));
+        o.bk[j] = (uint32_t)(r * 256 + 16 * (u ^ (r & 7)));
+    }
+    return o;
+}
+
+typedef EXKV_LDS uint8_t lds_u8;
+__device__ inline lds_u8* lds_ptr(uint32_t a) { return (lds_u8*)(uintptr_t)a; }
+__device__ inline uint4 lds16(const lds_u8* p) {
+    const u32x4 v = *reinterpret_cast<const EXKV_LDS u32x4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline void lds_st16(lds_u8* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    *reinterpret_cast<EXKV_LDS u32x4*>(p) = u32x4{a, b, c, d};
+}
+
+// Keep a rarely taken, wave-uniform branch as a branch: the compiler cannot move an
+// opaque volatile statement out of it, so it does not turn the block into selects that
+// would run on every page.
+__device__ inline void keep_branch() { asm volatile(""); }
+
+// ---- rebuild K or V of the staged page (lane = token r, channel group g)
+
+__device__ inline void stage_bytes(uint32_t sb, const LdsLane& o, int sm_off, int code_off, int base_off,
+                                   PageBytes& pb) {
+    pb.sm_lo = lds16(lds_ptr(sb + o.sml) + sm_off);
+    pb.sm_hi = lds16(lds_ptr(sb + o.smh) + sm_off);
+    pb.code = lds16(lds_ptr(sb + o.code) + code_off);
+    const lds_u8* bp = lds_ptr(sb + o.base) + base_off;
+    pb.b_lo = lds16(bp);
+    pb.b_hi = lds16(bp + 64);
+}
+
+__device__ inline void stage_bf16_k(uint32_t sb, const LdsLane& o, uint32_t out[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint4 v = lds16(lds_ptr(sb + o.bk[j]) + BS_K);
         out[4 * j] = v.x; out[4 * j + 1] = v.y; out[4 * j + 2] = v.z; out[4 * j + 3] = v.w;
     }
 }
 
-// V tile row r: logical 16-B unit u at physical unit u ^ ((r & 3) << 1)
-__device__ inline void write_v_tile(uint8_t* tile, int r, int g, const uint32_t v[16]) {
-    uint8_t* rp = tile + r * 256;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int u = (j < 2 ? 2 * g : 8 + 2 * g) + (j & 1);
-        *reinterpret_cast<u32x4*>(rp + 16 * (u ^ ((r & 3) << 1))) = u32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2],
-                                                                           v[4 * j + 3]};
-    }
+// The lane's 32 values of raw row q of a ring slot (channels 16g.. and 64+16g..)
+__device__ inline void lds_raw_values(uint32_t slot, int q, int g, uint32_t out[16]) {
+    const lds_u8* p = lds_ptr(slot + (uint32_t)(q * 256 + 32 * g));
+    const uint4 a0 = lds16(p), a1 = lds16(p + 16), h0 = lds16(p + 128), h1 = lds16(p + 144);
+    out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
+    out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
+    out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;
+    out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
+}
+
+// V tile row r (32 values of the lane) at the tile offset toff of the stage
+__device__ inline void write_v_tile(uint32_t sb, const LdsLane& o, int toff, const uint32_t v[16]) {
+    lds_u8* p = lds_ptr(sb + o.tw) + toff;
+    lds_st16(p, v[0], v[1], v[2], v[3]);
+    lds_st16(p + 16, v[4], v[5], v[6], v[7]);
+    lds_st16(p + 128, v[8], v[9], v[10], v[11]);
+    lds_st16(p + 144, v[12], v[13], v[14], v[15]);
 }
 
 // After a workgroup has written its partials: count it in; the last workgroup of the unit
@@ -257,15 +412,12 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
     __syncthreads();
     if (!s_last) return;
     __threadfence();                                   // acquire the other workgroups' partials
-    const int rows = a.HW * gh;
-    for (int idx = threadIdx.x; idx < rows * (kD / 2); idx += kThreads) {
-        const int dp = idx % (kD / 2);
-        const int h = (idx / (kD / 2)) % gh, hs = (idx / (kD / 2)) / gh;
+    const int rows = a.HW * gh, lane = threadIdx.x & 63;
+    for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {   // wavefront per row, lane = channel pair
+        const int h = i % gh, hs = i / gh;
         const int64_t row = (int64_t)b * a.Hq + (int64_t)(hb * a.HW + hs) * a.G + hg * 16 + h;
-        const float* m = a.part_m + row * a.nsplit;
-        const float M = split_max(m, a.nsplit);
-        reinterpret_cast<uint32_t*>(a.out + row * kD)[dp] =
-            merge_pair(a.part_o + row * a.nsplit * kD, m, a.part_l + row * a.nsplit, a.nsplit, M, dp);
+        reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] = merge_direct<kFusedMaxSplits>(
+            a.part_o + row * a.nsplit * kD, a.part_m + row * a.nsplit, a.part_l + row * a.nsplit, a.nsplit, lane);
     }
     if (threadIdx.x == 0) a.counters[blockIdx.y] = 0;  // ready for the next call on this workspace
     (void)split;
@@ -274,7 +426,9 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
 template <bool COMP>
 __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<COMP>::bytes];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+    __shared__ int progress[kWaves];                   // pages done per wavefront (priority hint)
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // uniform: scalar addressing
     // workgroup: sequence b, token split, block of HW KV heads (all read the same tokens, so
     // the workgroup's loads cover whole token rows of the [B, T, H, D] arrays); wavefront:
     // head slot w % HW, page phase w / HW
@@ -316,105 +470,197 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     // this wavefront's pages: p0 + phase + nphase * j, j < npw
     constexpr int NST = Ring<COMP>::nst;
     constexpr int STB = Ring<COMP>::stage;
-    uint8_t* ring = lds + wave * NST * STB;
+    const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<COMP>::per_wave);   // this wave's (uniform)
+    const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
+    const LdsLane lo = lds_lane_offsets(r, g);
     const int p0 = start / kPage;
     const int pend = end > start ? (end + kPage - 1) / kPage : p0;
     const int npw = pend - p0 > phase ? (pend - p0 - phase + nphase - 1) / nphase : 0;
     const int64_t rs = a.Hkv;
     const DmaLane dl = dma_lane_offsets<COMP>(lane, rs);
-    auto issue = [&](int j) {
+    const PairSrc basep = pair_src((uint64_t)(uintptr_t)a.k.base, (uint64_t)(uintptr_t)a.v.base);
+    const PairSrc rawp = pair_src((uint64_t)(uintptr_t)a.k.raw, (uint64_t)(uintptr_t)a.v.raw);
+    const PairSrc rawn = pair_src((uint64_t)a.k.raw_rows, (uint64_t)a.v.raw_rows);
+
+    // rowmask / rowoff: scalar loads (constant address space: read-only through the scalar
+    // cache, counted by lgkmcnt), three pages ahead of their page's compute
+    auto meta = [&](int j) {
+        PageMeta m{0u, 0u, 0, 0};
+        if constexpr (COMP) {
+            const int64_t page = ((int64_t)b * NP + p0 + phase + nphase * j) * rs + hk;
+            m.mk = (uint32_t)const_ld(a.k.rowmask + page);
+            m.ok = const_ld(a.k.rowoff + page);
+            m.mv = (uint32_t)const_ld(a.v.rowmask + page);
+            m.ov = const_ld(a.v.rowoff + page);
+        }
+        return m;
+    };
+    PageMeta m0{0u, 0u, 0, 0}, m1{0u, 0u, 0, 0}, m2{0u, 0u, 0, 0};   // pages j, j + 1, j + 2
+    if (COMP && npw > 0) m0 = meta(0);
+    if (COMP && npw > 1) m1 = meta(1);
+    if (COMP && npw > 2) m2 = meta(2);
+    auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
         const int pg = p0 + phase + nphase * j;
         const int64_t row0 = ((int64_t)b * a.TS + (int64_t)pg * kPage) * rs + hk;
         const int64_t page = ((int64_t)b * NP + pg) * rs + hk;
-        dma_page<COMP>(a, dl, row0, page, ring + (j % NST) * STB, lane);
+        dma_page<COMP>(a, dl, row0, page, sb, lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), basep, rawp, rawn);
     };
-#pragma unroll
-    for (int j = 0; j < NST - 1; ++j)
-        if (j < npw) issue(j);
+    if (npw > 0) issue(0, ring, m0);
+    if (NST == 3 && npw > 1) issue(1, ring + STB, m1);
     settle(qw);                                        // q (and the first pages) arrive here
     bf16x8 qop[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) qop[kc] = as_bf16x8(qw[4 * kc], qw[4 * kc + 1], qw[4 * kc + 2], qw[4 * kc + 3]);
 
+    progress[wave] = 0;
+    int stg = 0;                                       // stage of page j (j % NST)
     for (int j = 0; j < npw; ++j) {
-        // stage j is complete once only the younger pages' loads are in flight
-        if (NST == 3 && j + 1 < npw)
-            wait_vm<kDmaPerPage>();
-        else
+        // stage j is complete once only page j + 1's loads are in flight
+        if (NST == 3 && j + 1 < npw) {
+            if (COMP && raw_in_ring(m1))
+                wait_vm<kDmaPerPage[COMP] + 1>();
+            else
+                wait_vm<kDmaPerPage[COMP]>();
+        } else {
             wait_vm<0>();
-        uint8_t* st = ring + (j % NST) * STB;
+        }
+        const uint32_t sb = ring + (uint32_t)(stg * STB);
+        const int stn = stg == 0 ? NST - 1 : stg - 1;  // stage of page j + NST - 1
+        stg = stg == NST - 1 ? 0 : stg + 1;
         const int pg = p0 + phase + nphase * j;
         const int t0 = pg * kPage;
+        const bool ragged = t0 + kPage > end;          // uniform: only the last page of a split
         const bool row_valid = t0 + r < end;
+        const PageMeta mc = m0;
 
-        uint32_t kd[16], vd[16];
         uint32_t kraw[16], vraw[16];
-        uint32_t rmk = 0, rmv = 0;
-        if constexpr (COMP) {
-            const u32x4 meta = *reinterpret_cast<const u32x4*>(st + CS_META);
-            rmk = __builtin_amdgcn_readfirstlane(meta.x);
-            const int rok = __builtin_amdgcn_readfirstlane(meta.y);
-            rmv = __builtin_amdgcn_readfirstlane(meta.z);
-            const int rov = __builtin_amdgcn_readfirstlane(meta.w);
-            if ((rmk | rmv) != 0) {
-                // raw rows (a few percent of pages): fetch them now and wait, before the
-                // next page's loads go out, so the fixed wait counts stay exact
-                if ((rmk >> r) & 1u) load_raw_values(a.k.raw, raw_slot(rmk, rok, r, a.k.raw_rows), g, kraw);
-                if ((rmv >> r) & 1u) load_raw_values(a.v.raw, raw_slot(rmv, rov, r, a.v.raw_rows), g, vraw);
+        if (COMP && (mc.mk | mc.mv) != 0) {
+            if (raw_in_ring(mc)) {
+                // the page's raw rows came with it: entry of token r = its rank among the
+                // page's raw K rows (then V rows)
+                const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
+                const uint32_t below = (1u << r) - 1u;
+                if ((mc.mk >> r) & 1u) lds_raw_values(slot, __builtin_popcount(mc.mk & below), g, kraw);
+                if ((mc.mv >> r) & 1u)
+                    lds_raw_values(slot, __builtin_popcount(mc.mk) + __builtin_popcount(mc.mv & below), g, vraw);
+            } else {
+                // more raw rows than the ring slot holds (rare): fetch them now and wait, before
+                // the next page's loads go out, so the fixed wait counts stay exact
+                if ((mc.mk >> r) & 1u) load_raw_values(a.k.raw, raw_slot(mc.mk, mc.ok, r, a.k.raw_rows), g, kraw);
+                if ((mc.mv >> r) & 1u) load_raw_values(a.v.raw, raw_slot(mc.mv, mc.ov, r, a.v.raw_rows), g, vraw);
                 wait_vm<0>();
                 settle(kraw);
                 settle(vraw);
             }
         }
         if (j + NST - 1 < npw) {
-            // the recycled stage was last touched by this wavefront's LDS accesses of the
-            // previous page: let them finish before the DMA can land there
+            // the recycled stage and raw slot were last read by this wavefront's LDS accesses
+            // of this or the previous page: let them finish before the DMA can land there
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(j + NST - 1);
+            issue(j + NST - 1, ring + (uint32_t)(stn * STB), NST == 3 ? m2 : m1);
         }
-
-        // ---- K: rebuild, scores
         if constexpr (COMP) {
-            PageBytes pb;
-            stage_bytes(st, CS_KSM, CS_KCODE, CS_BASE, r, g, pb);
-            rebuild_values(pb, kd);
-            if (rmk != 0 && ((rmk >> r) & 1u)) {       // page with raw rows (uniform test first)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) kd[i] = kraw[i];
-            }
-        } else {
-            stage_bf16_k(st, r, g, kd);
+            m0 = m1;
+            m1 = m2;
+            if (j + 3 < npw) m2 = meta(j + 3);
         }
-        const bool ragged = t0 + kPage > end;          // uniform: only the last page of a split
-        if (ragged && !row_valid) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) kd[i] = 0u;
+        // Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one, and
+        // the older one's first loads are also served first: left alone it runs ahead and its
+        // partner finishes last. The one that is behind takes the higher priority.
+        if (j > 0) {
+            const int other = progress[wave ^ 4];
+            if (j < other)
+                __builtin_amdgcn_s_setprio(2);
+            else
+                __builtin_amdgcn_s_setprio(0);
         }
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc)
-            sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
+        progress[wave] = j;
 
-        // ---- online softmax: lane = head r, tokens t0 + 4g + i
-        float sc[4];
+        // ---- K and V bytes out of the stage together; the V reads overlap the K rebuild
+        uint32_t kd[16], vd[16];
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (COMP) {
+            PageBytes pk, pv;
+            stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
+            stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
+            rebuild_values(pk, kd);
+            if (mc.mk != 0) {                          // page with raw K rows
+                keep_branch();
+                if ((mc.mk >> r) & 1u) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = sa[i] * a.qk_scale;
+                    for (int i = 0; i < 16; ++i) kd[i] = kraw[i];
+                }
+            }
+            if (ragged) {                              // rows past the end of the split: zero
+                keep_branch();
+                if (!row_valid) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) kd[i] = 0u;
+                }
+            }
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc)
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
+            // V rebuild while the score MFMAs run; the tile overwrites the K bytes (read above)
+            rebuild_values(pv, vd);
+            if (mc.mv != 0) {
+                keep_branch();
+                if ((mc.mv >> r) & 1u) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) vd[i] = vraw[i];
+                }
+            }
+            if (ragged) {
+                keep_branch();
+                if (!row_valid) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) vd[i] = 0u;
+                }
+            }
+            write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
+        } else {
+            stage_bf16_k(sb, lo, kd);
+            if (ragged) {
+                keep_branch();
+                if (!row_valid) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) kd[i] = 0u;
+                }
+            }
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc)
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
+            if (ragged) {                              // ragged last page: zero the V rows past the end
+                keep_branch();
+                if (!row_valid) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) vd[i] = 0u;
+                    write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
+                }
+            }
+        }
+
+        // ---- online softmax: lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
+        // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into
+        // the exponent's fma: p = 2^(s * scale - m).
+        float sc[4] = {sa[0], sa[1], sa[2], sa[3]};
         if (ragged) {
+            keep_branch();
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (t0 + 4 * g + i >= end) sc[i] = -INFINITY;
         }
         float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        mloc = group_max(mloc) * a.qk_scale;
         const float m_new = fmaxf(m_i, mloc);
         const float alpha = fast_exp2(m_i - m_new);
         float psum = 0.f;
         bf16x4 pb4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(sc[i] - m_new);
+            const float p = fast_exp2(__builtin_fmaf(sc[i], a.qk_scale, -m_new));
             psum += p;
             pb4[i] = (__bf16)p;
         }
@@ -425,44 +671,18 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
         }
 
-        // ---- V: rebuild into the stage's bf16 tile (compressed) or use the staged rows
-        uint8_t* tile = st + Ring<COMP>::vtile;
-        if constexpr (COMP) {
-            PageBytes pv;
-            stage_bytes(st, CS_VSM, CS_VCODE, CS_BASE + 128, r, g, pv);
-            rebuild_values(pv, vd);
-            if (rmv != 0 && ((rmv >> r) & 1u)) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) vd[i] = vraw[i];
-            }
-            if (ragged && !row_valid) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) vd[i] = 0u;
-            }
-            write_v_tile(tile, r, g, vd);
-        } else {
-            if (ragged && !row_valid) {                // ragged last page: zero the rows past the end
-#pragma unroll
-                for (int i = 0; i < 16; ++i) vd[i] = 0u;
-                write_v_tile(tile, r, g, vd);
-            }
-        }
         // ---- O^T += V^T P^T: V^T rows 4g..4g+3 of channel 16nb + r via the transpose read
         const s16x4 pop = __builtin_bit_cast(s16x4, pb4);
-        const int trow = 4 * g + (r >> 2);
-        const uint8_t* trp = tile + trow * 256 + 8 * (r & 1);
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) {
-            const int u = 2 * nb + ((r & 3) >> 1);
-            const s16x4 av =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)(trp + 16 * (u ^ ((trow & 3) << 1))));
+            const lds_u8* tp = lds_ptr(sb + lo.tr[nb & 3]) + Ring<COMP>::vtile + (nb >= 4 ? 128 : 0);
+            const s16x4 av = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)tp);
             acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pop, acc[nb], 0, 0, 0);
         }
     }
 
     // ---- merge the page phases of each head (same algebra as the split merge)
-    float l_t = l_i + __shfl_xor(l_i, 16);
-    l_t = l_t + __shfl_xor(l_t, 32);
+    const float l_t = group_sum(l_i);
     const int gh = min(16, a.G - hg * 16);
     const int64_t hq0 = (int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16;     // first query head of this wave
     if (nphase == 1) {                                 // one wavefront per head: write its partial
@@ -521,10 +741,8 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
 __global__ void __launch_bounds__(64) attn_reduce_kernel(const float* po, const float* pm, const float* pl,
                                                          uint16_t* out, int ns) {
     const int64_t row = blockIdx.x;
-    const float* m = pm + row * ns;
-    const float M = split_max(m, ns);
     reinterpret_cast<uint32_t*>(out + row * kD)[threadIdx.x] =
-        merge_pair(po + row * ns * kD, m, pl + row * ns, ns, M, threadIdx.x);
+        merge_row(po + row * ns * kD, pm + row * ns, pl + row * ns, ns, threadIdx.x);
 }
 
 }  // namespace exkv
@@ -639,7 +857,7 @@ extern "C" int exkv_attn_compressed(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, E
     int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed: null output");
-    if (ws_cnt) {                                      // merge fused into the split kernel
+    if (ws_cnt && nsplit <= kFusedMaxSplits) {         // merge fused into the split kernel
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(true, a, stream);
@@ -660,7 +878,7 @@ extern "C" int exkv_attn_bf16(const void* q, const void* k, const void* v, float
     int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16: null output");
-    if (ws_cnt) {
+    if (ws_cnt && nsplit <= kFusedMaxSplits) {
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(false, a, stream);

@@ -75,9 +75,10 @@ int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, cons
 /* Split-K GQA decode attention over compressed K and V caches, then the split merge.
  * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
  * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: B*(Hkv/gcd(Hkv,8))*ceil(Hq/Hkv/16) i32 arrival
- * counters, all zero before the first call (each call leaves them zero); with ws_cnt the
- * merge runs inside the split kernel (its last workgroup per unit), with ws_cnt == NULL as
- * a second kernel (same bits). Calls that share a workspace must not overlap.
+ * counters, all zero before the first call (each call leaves them zero); with ws_cnt and
+ * nsplit <= 4 the merge runs inside the split kernel (its last workgroup per unit),
+ * otherwise as a second kernel (same bits; ws_cnt may be NULL). Calls that share a
+ * workspace must not overlap.
  * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
  * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
  * qk_scale = 128^-1/2 * log2(e). Bit-identical to exkv_attn_bf16 on the decoded contents.

@@ -36,6 +36,20 @@ WORKLOADS = {   # name: (B, T, TS, Hq, Hkv, description)
 }
 
 
+def profiled_traffic(workload):
+    """HBM bytes per split-kernel launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary of this workload (scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"attn_split_{workload}_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if d.get("workload") != workload:
+        return None, None
+    return int(d["traffic_bytes"]), os.path.relpath(path, ROOT)
+
+
 def cpu_model():
     try:
         for ln in open("/proc/cpuinfo"):
@@ -211,6 +225,7 @@ def main():
     enc = encoder_gbps(exactkv, kernels, kbs[0], T, a.steps, a.warmup)
     print("[bench] encoder timed", file=sys.stderr, flush=True)
 
+    traffic, traffic_src = profiled_traffic(a.workload)
     res = {
         "metric": METRIC, "value": round(ms_c * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_c, 5), "higher_is_better": False, "scaling": "weak",
@@ -219,7 +234,7 @@ def main():
                    "head_dim": 128, "page": 16, "nsplit": ns, "split_len": sl, "cache_copies": a.copies,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
                      "kernel_us": round(ms_split * 1e3, 2)},
         "timing": "HIP events around back-to-back calls on one stream",

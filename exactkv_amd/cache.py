@@ -130,11 +130,21 @@ class CompressedKV:
 
     def append(self, x):
         """x: [B, H, D] bf16, one new token per sequence."""
+        self._check_can_append()
+        self._check_token(x)
+        self._launch_append(x)
+        self._advance()
+
+    def _check_can_append(self):
         assert self._pending is None, "call check_overflow() after a page boundary before appending again"
         assert self.T < self.TS, "cache is full"
+
+    def _check_token(self, x):
         if x.shape != (self.B, self.H, self.D) or x.dtype != torch.bfloat16 or x.stride(2) != 1:
             raise ValueError(f"append expects a bf16 [{self.B}, {self.H}, {self.D}] tensor with contiguous rows")
-        self._launch_append(x)
+
+    def _advance(self):
+        """Host side of an append whose kernels already ran (directly or in a graph replay)."""
         self.T += 1
         if self.T % P == 0:
             self._pending = self.T // P - 1
@@ -184,10 +194,19 @@ class BF16KV:
         self.state[0] = self.T
 
     def append(self, x):
+        self._check_can_append()
+        self._check_token(x)
+        self._launch_append(x)
+        self._advance()
+
+    def _check_can_append(self):
         assert self.T < self.TS, "cache is full"
+
+    def _check_token(self, x):
         if x.shape != (self.B, self.H, self.D) or x.dtype != torch.bfloat16 or x.stride(2) != 1:
             raise ValueError(f"append expects a bf16 [{self.B}, {self.H}, {self.D}] tensor with contiguous rows")
-        self._launch_append(x)
+
+    def _advance(self):
         self.T += 1
 
     def _launch_append(self, x):

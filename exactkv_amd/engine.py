@@ -1,0 +1,187 @@
+"""Batched greedy decoding for Hugging Face Llama-3 / Qwen2 / Qwen2.5 / Qwen3 models over
+the compressed (or bf16) KV cache -- drop-in for the reference's exactkv/engine.py:18-95.
+
+The model's own weights and modules are used; only the KV cache and decode attention
+are replaced, so two engines that differ only in the cache produce identical tokens and
+logits wherever the cache is lossless (here: always, bit for bit).
+
+MI355X specifics:
+  * a decode step depends on no host value: the position comes from the cache's device
+    token count, appends read it there, and attention gets it through `lens`. The first
+    decode step runs eagerly on the engine's stream (it sets up BLAS handles and the
+    attention workspaces there); the next one is captured in a HIP graph, and every
+    later step replays it. A pool growth at a page boundary changes the raw-pool
+    buffers, so the graph is captured again on the next step;
+  * prefill runs one sequence at a time through the model's own forward pass, with SDPA
+    restricted to its fused (flash / memory-efficient) kernels.
+"""
+import importlib
+
+import torch
+
+from .cache import BF16KV, CompressedKV, check_overflow
+from .kernels import attention_compressed, attention_reference, P
+
+BACKENDS = {"exactkv": CompressedKV, "bf16": BF16KV}
+
+
+def _fused_sdpa():
+    """Context restricting scaled_dot_product_attention to its fused kernels (it raises
+    instead of falling back to the unfused math path)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    return sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION])
+
+
+class Engine:
+    def __init__(self, model, B, T_max, backend="exactkv", attn=None, before_step=None, graph=True):
+        """backend: 'exactkv' / 'bf16', or a cache class with the same interface.
+        attn(q, k_cache, v_cache) and before_step(engine, T) let benchmarks plug in other
+        kernels (reference engine.py:30-33); with either plug-in the step runs eagerly.
+        graph: capture the decode step in a HIP graph (default)."""
+        cfg = model.config
+        self.m = model
+        self.L, self.Hq, self.Hkv = cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads
+        self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.Hq
+        assert cfg.model_type in ("qwen2", "qwen3", "llama"), \
+            f"supported: Qwen2/2.5, Qwen3, Llama-3 (got {cfg.model_type})"
+        assert not getattr(cfg, "use_sliding_window", False), "sliding-window attention is not supported"
+        assert self.D == 128, "head dim 128 only"
+        self.B, self.TS = B, -(-T_max // P) * P
+        self.dev = next(model.parameters()).device
+        cls = BACKENDS.get(backend, backend)
+        kw = {"device": self.dev} if isinstance(cls, type) and issubclass(cls, (CompressedKV, BF16KV)) else {}
+        self.kv = [(cls(B, self.TS, self.Hkv, self.D, **kw), cls(B, self.TS, self.Hkv, self.D, **kw))
+                   for _ in range(self.L)]
+        self.attn = attn
+        self.before_step = before_step
+        self.rope = importlib.import_module(type(model.model.layers[0].self_attn).__module__).apply_rotary_pos_emb
+        self.qk_norm = hasattr(model.model.layers[0].self_attn, "k_norm")   # Qwen3
+        self.grows = 0
+        ours = isinstance(cls, type) and issubclass(cls, (CompressedKV, BF16KV))
+        self.use_graph = bool(graph) and attn is None and before_step is None and ours
+        self._stream = torch.cuda.Stream(device=self.dev) if self.use_graph else None
+        self._graph = None
+        self._graph_key = None
+        self._warm = False
+        self._tok = torch.zeros(B, dtype=torch.long, device=self.dev)
+        self._pos = torch.zeros(1, 1, dtype=torch.long, device=self.dev)
+        self._logits = None
+
+    # ---------------------------------------------------------------- prefill
+    @torch.no_grad()
+    def prefill(self, ids):
+        """ids: [B, T] token ids. Returns the greedy next token of each sequence, [B]."""
+        nxt = []
+        with _fused_sdpa():
+            for b in range(ids.shape[0]):
+                out = self.m.model(ids[b:b + 1], use_cache=True)
+                pkv = out.past_key_values
+                for i in range(self.L):
+                    lay = pkv.layers[i] if hasattr(pkv, "layers") else None
+                    k, v = (lay.keys, lay.values) if lay is not None else (pkv.key_cache[i], pkv.value_cache[i])
+                    self.kv[i][0].prefill_slot(b, k.transpose(1, 2).contiguous())
+                    self.kv[i][1].prefill_slot(b, v.transpose(1, 2).contiguous())
+                nxt.append(self.m.lm_head(self.m.model.norm(out.last_hidden_state[:, -1])).argmax(-1))
+                del out, pkv
+        self._graph = None                      # buffers may have grown
+        return torch.cat(nxt)
+
+    # ---------------------------------------------------------------- decode step
+    def _attend(self, q, kc, vc):
+        if self.attn is not None:
+            return self.attn(q, kc, vc)
+        lens = kc.state[:1]                     # token count on the device (after this step's append)
+        if isinstance(kc, CompressedKV):
+            return attention_compressed(q, kc, vc, kc.TS, lens=lens)
+        return attention_reference(q, kc.buf, vc.buf, kc.TS, lens=lens)
+
+    def _forward(self, tok, device_only):
+        """One decode step: tok [B] -> logits [B, vocab]. device_only: appends launch their
+        kernels only (the host counts advance after the step), so the step reads no host
+        state that changes between steps and can be captured; otherwise each append also
+        advances its cache's host count, as the reference does, so an attention plug-in
+        sees the current length."""
+        m, B, Hq, Hkv, D = self.m, self.B, self.Hq, self.Hkv, self.D
+        h = m.model.embed_tokens(tok.view(B, 1))
+        self._pos.copy_(self.kv[0][0].state[:1].view(1, 1))                 # position = tokens so far
+        cos, sin = m.model.rotary_emb(h, self._pos)
+        for i, layer in enumerate(m.model.layers):
+            att = layer.self_attn
+            x = layer.input_layernorm(h)
+            q = att.q_proj(x).view(B, 1, Hq, D)
+            k = att.k_proj(x).view(B, 1, Hkv, D)
+            v = att.v_proj(x).view(B, 1, Hkv, D)
+            if self.qk_norm:
+                q, k = att.q_norm(q), att.k_norm(k)
+            q, k = self.rope(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+            kc, vc = self.kv[i]
+            if device_only:
+                kc._check_token(k[:, :, 0])
+                vc._check_token(v[:, 0])
+                kc._launch_append(k[:, :, 0])
+                vc._launch_append(v[:, 0])
+            else:
+                kc.append(k[:, :, 0])
+                vc.append(v[:, 0])
+            o = self._attend(q[:, :, 0].contiguous(), kc, vc)
+            h = h + att.o_proj(o.reshape(B, 1, Hq * D))
+            h = h + layer.mlp(layer.post_attention_layernorm(h))
+        return m.lm_head(m.model.norm(h))[:, 0]
+
+    def _buffers_key(self):
+        return tuple(c.raw.data_ptr() for kv in self.kv for c in kv if isinstance(c, CompressedKV))
+
+    def _advance(self):
+        for kv in self.kv:
+            for c in kv:
+                c._advance()
+
+    @torch.no_grad()
+    def step(self, tok):
+        """tok: [B] current tokens. Returns logits [B, vocab] (bf16) for the next token."""
+        T = self.kv[0][0].T
+        if self.use_graph:
+            for kv in self.kv:
+                for c in kv:
+                    c._check_can_append()
+        if self.before_step:
+            self.before_step(self, T + 1)
+        if not self.use_graph:
+            logits = self._forward(tok, device_only=False)
+        else:
+            cur = torch.cuda.current_stream(self.dev)
+            self._stream.wait_stream(cur)
+            with torch.cuda.stream(self._stream):
+                self._tok.copy_(tok)
+                if not self._warm:                       # first step: eager, on the graph's stream
+                    logits = self._forward(self._tok, device_only=True)
+                    self._warm = True
+                else:
+                    key = self._buffers_key()
+                    if self._graph is None or key != self._graph_key:
+                        self._graph = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(self._graph, stream=self._stream):
+                            self._logits = self._forward(self._tok, device_only=True)
+                        self._graph_key = key
+                    self._graph.replay()
+                    logits = self._logits.clone()
+            cur.wait_stream(self._stream)
+            self._advance()
+        if (T + 1) % P == 0:
+            self.grows += check_overflow([c for kv in self.kv for c in kv])
+        return logits
+
+    @torch.no_grad()
+    def generate(self, ids, n_new):
+        """Greedy decoding: returns (tokens [B, n_new], logits [B, n_new - 1, vocab])."""
+        t = self.prefill(ids)
+        toks, logits = [t], []
+        for _ in range(n_new - 1):
+            lg = self.step(t)
+            logits.append(lg)
+            t = lg.argmax(-1)
+            toks.append(t)
+        return torch.stack(toks, 1), torch.stack(logits, 1)
+
+    def kv_bytes(self):
+        return sum(c.nbytes() for kv in self.kv for c in kv)

@@ -1,0 +1,114 @@
+"""Engine (reference exactkv/engine.py:18-95, tests/test_exactkv.py:107-122): greedy decoding
+of small random-init Llama-3 / Qwen3 / Qwen2 models over the compressed and the bf16 cache.
+
+  * the two backends give the same tokens and bit-identical logits (the cache is lossless
+    and the two attention kernels are bit-identical);
+  * HIP-graph replay of the step equals eager steps bit for bit;
+  * a raw-pool growth between steps makes the engine capture the step again, and the
+    results stay exact;
+  * an attention plug-in (reference engine.py:30-33) runs the step eagerly.
+
+Prompts are 37 tokens (a partly filled page) and 40 tokens are generated, so the run
+crosses two page boundaries (page encodes inside the step, check_overflow after it)."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+B, PROMPT, NEW = 3, 37, 40
+
+
+def _model(kind, layers=2, seed=0):
+    from transformers import (LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM, Qwen3Config,
+                              Qwen3ForCausalLM)
+    common = dict(vocab_size=1024, hidden_size=512, intermediate_size=1024, num_hidden_layers=layers,
+                  num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=4096)
+    if kind == "llama":
+        cfg, cls = LlamaConfig(rope_theta=5e5, **common), LlamaForCausalLM
+    elif kind == "qwen3":
+        cfg, cls = Qwen3Config(head_dim=128, rope_theta=1e6, **common), Qwen3ForCausalLM
+    else:
+        cfg, cls = Qwen2Config(rope_theta=1e6, **common), Qwen2ForCausalLM
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        m = cls(cfg)
+    return m.to(torch.bfloat16).eval()
+
+
+def _ids(vocab=1024, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (B, PROMPT), generator=g).cuda()
+
+
+def _run(model, backend, graph=True, **kw):
+    import exactkv_amd as exactkv
+    eng = exactkv.Engine(model, B, PROMPT + NEW, backend=backend, graph=graph, **kw)
+    toks, logits = eng.generate(_ids(), NEW)
+    torch.cuda.synchronize()
+    return eng, toks, logits
+
+
+@pytest.mark.parametrize("kind", ["llama", "qwen3", "qwen2"])
+def test_backends_give_identical_tokens_and_logits(kind):
+    m = _model(kind)
+    print(f"[engine] {kind}: bf16 backend", flush=True)
+    _, tb, lb = _run(m, "bf16")
+    print(f"[engine] {kind}: exactkv backend", flush=True)
+    e, tc, lc = _run(m, "exactkv")
+    assert torch.equal(tb, tc)
+    assert torch.equal(lb.view(torch.int16), lc.view(torch.int16))
+    assert torch.isfinite(lc.float()).all()
+    assert e.kv[0][0].T == PROMPT + NEW - 1
+
+
+def test_graph_replay_equals_eager_steps():
+    m = _model("llama")
+    print("[engine] eager", flush=True)
+    ee, te, le = _run(m, "exactkv", graph=False)
+    print("[engine] graph", flush=True)
+    eg, tg, lg = _run(m, "exactkv", graph=True)
+    assert eg.use_graph and eg._graph is not None and not ee.use_graph
+    assert torch.equal(te, tg)
+    assert torch.equal(le.view(torch.int16), lg.view(torch.int16))
+
+
+def test_pool_growth_between_steps_recaptures_and_stays_exact():
+    import exactkv_amd as exactkv
+    m = _model("llama")
+    ids = _ids()
+    ref = exactkv.Engine(m, B, PROMPT + NEW, backend="bf16")
+    eng = exactkv.Engine(m, B, PROMPT + NEW, backend="exactkv")
+    t_r, t_e = ref.prefill(ids), eng.prefill(ids)
+    assert torch.equal(t_r, t_e)
+    keys = set()
+    for s in range(NEW - 1):
+        if s in (3, 17):                      # grow two pools between steps
+            c = eng.kv[s % 2][1]
+            cap = c.cap
+            c._grow(c.cap + 1)
+            assert c.cap > cap
+        lr, le = ref.step(t_r), eng.step(t_e)
+        assert torch.equal(lr.view(torch.int16), le.view(torch.int16)), s
+        if eng._graph_key is not None:
+            keys.add(eng._graph_key)
+        t_r, t_e = lr.argmax(-1), le.argmax(-1)
+    assert len(keys) >= 3                     # captured, then captured again after each growth
+
+
+def test_attention_plugin_runs_eagerly():
+    import exactkv_amd as exactkv
+    m = _model("llama")
+    calls = []
+
+    def attn(q, kc, vc):
+        calls.append(kc.T)
+        return exactkv.decode_attention(q, kc, vc)
+
+    _, tb, lb = _run(m, "bf16", attn=attn)
+    calls.clear()
+    e, tp, lp = _run(m, "exactkv", attn=attn)
+    assert not e.use_graph
+    assert len(calls) == 2 * (NEW - 1)       # layers x steps
+    assert calls[0] == PROMPT + 1 and calls[-1] == PROMPT + NEW - 1
+    assert torch.equal(tb, tp)
+    assert torch.equal(lb.view(torch.int16), lp.view(torch.int16))

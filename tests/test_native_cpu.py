@@ -71,3 +71,10 @@ def test_rebuild_bitmath_exhaustive(tmp_path):
     assert r.returncode == 0, r.stdout
     assert "0 mismatches" in r.stdout
     assert ctypes is not None
+
+
+def test_engine_module_imports_without_a_gpu():
+    import exactkv_amd as exactkv
+    from exactkv_amd import engine
+    assert exactkv.Engine is engine.Engine
+    assert set(engine.BACKENDS) == {"exactkv", "bf16"}

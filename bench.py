@@ -155,7 +155,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["e2e"])
+    ap.add_argument("--e2e-prompt", type=int, default=4096)
+    ap.add_argument("--e2e-gen", type=int, default=256)
+    ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
+    ap.add_argument("--e2e-work-gib", type=float, default=6.0,
+                    help="memory kept free beyond the caches for activations, logits and pool growth")
     ap.add_argument("--copies", type=int, default=4, help="cache copies rotated to defeat the 256 MB MALL")
     ap.add_argument("--cpu-seqs", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -164,6 +169,11 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
+    if a.workload == "e2e":
+        if a.gpus != 1:
+            print("bench.py measures one GPU", file=sys.stderr)
+            sys.exit(2)
+        return e2e(a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -272,6 +282,97 @@ def profile_run(kernels, q, kc, vc, kb, vb, T, ns, sl, out):
     torch.cuda.synchronize()
     print(json.dumps({"profile_run": True, "copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
                       "nsplit": ns, "split_len": sl}), flush=True)
+
+
+E2E_CONFIG = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                  num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
+                  rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=False)
+
+
+def e2e(a):
+    """Config 4: batched greedy decoding with the engine on a random-init Llama-3.1-8B
+    (weights N(0, 0.02) bf16), prompts of uniform random token ids, the reference's
+    protocol (bench/e2e.py:43-101): KV budget = free memory after the weights minus
+    1.6 GiB, KV per sequence = kv_bytes(B=2) - kv_bytes(B=1), each backend at the largest
+    batch that fits, then the compressed cache also at the bf16 batch (same work)."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import exactkv_amd as exactkv
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    PL, G = a.e2e_prompt, a.e2e_gen
+    TM = PL + G
+    print(f"[e2e] building random-init Llama-3.1-8B", file=sys.stderr, flush=True)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(LlamaConfig(**E2E_CONFIG)).to(torch.bfloat16).eval()
+    torch.cuda.empty_cache()
+    wbytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    budget = torch.cuda.mem_get_info()[0] - 1.6 * 2**30
+
+    def per_seq(be):
+        e1, e2 = exactkv.Engine(model, 1, TM, backend=be), exactkv.Engine(model, 2, TM, backend=be)
+        d = e2.kv_bytes() - e1.kv_bytes()
+        del e1, e2
+        torch.cuda.empty_cache()
+        return d
+    ps = {be: per_seq(be) for be in ("bf16", "exactkv")}
+    fit = {be: int(budget // ps[be]) for be in ps}
+    # working memory beyond the caches (prefill activations, logits, pool growth)
+    work = a.e2e_work_gib * 2**30
+    run_b = {be: max(1, min(fit[be], int((budget - work) // ps[be]))) for be in ps}
+    if a.e2e_batch:
+        run_b = {be: min(a.e2e_batch, run_b[be]) for be in ps}
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, E2E_CONFIG["vocab_size"], (max(run_b.values()), PL), generator=g).to(dev)
+
+    def run(be, B):
+        eng = exactkv.Engine(model, B, TM, backend=be)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        nxt = []
+        for b0 in range(0, B, 64):
+            nxt.append(eng.prefill(ids[b0:min(B, b0 + 64)], b0=b0))
+            print(f"[e2e] {be} B={B}: prefilled {min(B, b0 + 64)}", file=sys.stderr, flush=True)
+        t = torch.cat(nxt)
+        torch.cuda.synchronize()
+        t1 = time.time()
+        toks = [t]
+        for s in range(G - 1):
+            t = eng.step(t).argmax(-1)
+            toks.append(t)
+            if s % 64 == 63:
+                print(f"[e2e] {be} B={B}: step {s + 1}", file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        t2 = time.time()
+        r = dict(backend=be, batch=B, kv_mib_per_seq=round(ps[be] / 2**20, 1),
+                 ms_per_step=round((t2 - t1) / (G - 1) * 1e3, 2),
+                 decode_tokens_per_s=round(B * (G - 1) / (t2 - t1), 1), prefill_s=round(t1 - t0, 1),
+                 pool_grows=eng.grows)
+        print(json.dumps(r), file=sys.stderr, flush=True)
+        out = torch.stack(toks, 1).cpu()
+        del eng
+        torch.cuda.empty_cache()
+        return r, out
+
+    r_b, tok_b = run("bf16", run_b["bf16"])
+    r_c, tok_c = run("exactkv", run_b["exactkv"])
+    r_s, tok_s = run("exactkv", r_b["batch"])
+    res = {
+        "metric": "e2e greedy decode tok/s (Llama-3.1-8B random init, 4096-token prompts, 256 new tokens)",
+        "value": r_c["decode_tokens_per_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights N(0,0.02), random token ids)",
+        "config": {"workload": "c4: Llama-3.1-8B e2e greedy decode", "prompt": PL, "gen": G,
+                   "weights_gib": round(wbytes / 2**30, 2), "kv_budget_gib": round(budget / 2**30, 2),
+                   "sequences_fit": fit, "batch_run": run_b},
+        "rows": [r_b, r_c, r_s],
+        "throughput_ratio": round(r_c["decode_tokens_per_s"] / r_b["decode_tokens_per_s"], 3),
+        "step_time_ratio_same_batch": round(r_b["ms_per_step"] / r_s["ms_per_step"], 3),
+        "tokens_equal_same_batch": bool(torch.equal(tok_b, tok_s)),
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(res), flush=True)
 
 
 def split_only(kernels, q, kc, vc, T, ns, sl, compressed):

@@ -69,12 +69,15 @@ class Engine:
 
     # ---------------------------------------------------------------- prefill
     @torch.no_grad()
-    def prefill(self, ids):
-        """ids: [B, T] token ids. Returns the greedy next token of each sequence, [B]."""
+    def prefill(self, ids, b0=0):
+        """ids: [B, T] token ids. Returns the greedy next token of each sequence, [B].
+        b0 (additive): fill sequence slots b0.. with ids' rows, so a long prefill can be
+        done in pieces (slot 0 first)."""
         nxt = []
         with _fused_sdpa():
-            for b in range(ids.shape[0]):
-                out = self.m.model(ids[b:b + 1], use_cache=True)
+            for i0 in range(ids.shape[0]):
+                b = b0 + i0
+                out = self.m.model(ids[i0:i0 + 1], use_cache=True)
                 pkv = out.past_key_values
                 for i in range(self.L):
                     lay = pkv.layers[i] if hasattr(pkv, "layers") else None

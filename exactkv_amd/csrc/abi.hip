@@ -48,7 +48,11 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
         m = t;
     }
     const int64_t units = (int64_t)B * (Hkv / hw) * hg;
-    int64_t ns = (target_blocks + units - 1) / units;
+    // Up to target_blocks units: one round of about target_blocks workgroups (one per CU).
+    // More units than that: several rounds are unavoidable, so aim at 8 rounds, which
+    // hides the rounding of the last round and staggers the workgroups' start-up.
+    int64_t ns = units < target_blocks ? (target_blocks + units - 1) / units
+                                       : (8 * (int64_t)target_blocks + units - 1) / units;
     const int64_t cap = ((int64_t)T + min_split - 1) / min_split;
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;

@@ -34,8 +34,10 @@ def choose_split(B, Hkv, T, BLOCK_N, target=512):
 
 
 def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=256):
-    """MI355X split plan (native): about `target_blocks` workgroups (one per CU), at least
-    `min_split` tokens per split, split length a multiple of 32. Returns (nsplit, split_len)."""
+    """MI355X split plan (native): about `target_blocks` workgroups (one per CU) -- or about
+    8x that many when there are more (sequence, head-block) units than workgroups in one
+    round -- at least `min_split` tokens per split, split length a multiple of 32.
+    Returns (nsplit, split_len)."""
     ns, sl = ctypes.c_int32(), ctypes.c_int32()
     _lib.call("exkv_plan_splits", B, Hkv, Hq, T, target_blocks, min_split, ctypes.byref(ns), ctypes.byref(sl))
     return ns.value, sl.value
@@ -61,7 +63,10 @@ def merge_units(B, Hkv, Hq):
     return B * (Hkv // math.gcd(Hkv, 8)) * (-(-(Hq // Hkv) // 16))
 
 
-FUSED_MERGE_MAX_SPLITS = 4   # up to this many splits the split kernel's last workgroup merges
+FUSED_MERGE_MAX_SPLITS = 4   # up to this many splits the split kernel's last workgroup can merge
+FUSED_MERGE_MAX_BLOCKS = 256  # ... and only within one round of workgroups: the merging workgroup's
+#                               device-scope fences write back its L2, which costs more than the
+#                               separate merge launch once many workgroups do it
 
 
 def _counters(dev, units):
@@ -70,6 +75,14 @@ def _counters(dev, units):
     if c is None:
         c = _CNT[key] = torch.zeros(units, dtype=torch.int32, device=dev)
     return c
+
+
+def _fused_counters(dev, B, Hkv, Hq, ns):
+    """Arrival counters when the merge runs in the split kernel's tail, else None."""
+    units = merge_units(B, Hkv, Hq)
+    if ns > FUSED_MERGE_MAX_SPLITS or units * ns > FUSED_MERGE_MAX_BLOCKS:
+        return None
+    return _counters(dev, units)
 
 
 def _check_q(q):
@@ -129,7 +142,7 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
-    cnt = _counters(q.device, merge_units(B, Hkv, Hq)) if ns <= FUSED_MERGE_MAX_SPLITS else None
+    cnt = _fused_counters(q.device, B, Hkv, Hq, ns)
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
               cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
@@ -150,7 +163,7 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
-    cnt = _counters(q.device, merge_units(B, Hkv, Hq)) if ns <= FUSED_MERGE_MAX_SPLITS else None
+    cnt = _fused_counters(q.device, B, Hkv, Hq, ns)
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
               wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl,

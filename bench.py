@@ -60,17 +60,22 @@ def cpu_model():
     return platform.processor()
 
 
-def algorithmic_bytes(caches, B, T, Hq, Hkv):
+def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None):
     """Bytes a decode-attention call must move: per K/V cache and valid token row
     128 (sm) + 64 (code); per touched page and head 128 (base) + 8 (rowmask, rowoff);
-    256 per raw row referenced; plus q and the output."""
+    256 per raw row referenced; plus q and the output. lens: per-sequence lengths."""
     import torch
-    npg = -(-T // 16)
+    lens = [T] * B if lens is None else [int(x) for x in lens]
     total = 0
     for c in caches:
-        rm = c.rowmask[:B, :npg].to(torch.int64)
-        raw_rows = int(sum(((rm >> i) & 1).sum().item() for i in range(16)))
-        total += B * T * Hkv * 192 + B * npg * Hkv * 136 + raw_rows * 256
+        for b, L in enumerate(lens):
+            npg = -(-L // 16)
+            rm = c.rowmask[b, :npg].to(torch.int64)                        # [npg, Hkv]
+            bit = torch.arange(16, device=rm.device)
+            tok = torch.arange(npg, device=rm.device)[:, None] * 16 + bit     # [npg, 16]
+            raw = (rm[:, :, None] >> bit) & 1                                 # [npg, Hkv, 16]
+            raw_rows = int((raw * (tok < L)[:, None, :]).sum().item())
+            total += L * Hkv * 192 + npg * Hkv * 136 + raw_rows * 256
     return total + 2 * B * Hq * 128 * 2
 
 
@@ -155,7 +160,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["e2e"])
+    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -169,11 +174,11 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload == "e2e":
+    if a.workload in ("e2e", "c3"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
-        return e2e(a)
+        return e2e(a) if a.workload == "e2e" else c3_stress(a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -284,6 +289,72 @@ def profile_run(kernels, q, kc, vc, kb, vb, T, ns, sl, out):
                       "nsplit": ns, "split_len": sl}), flush=True)
 
 
+def c3_stress(a):
+    """Config 3 (Qwen3-8B shape): 32q/8kv, B32 x 4096, per-sequence lengths U[3500, 4096]
+    (seeded), outlier-row rate 0.6%, raw pool started small (reserve 1e-4) so prefill
+    grows it several times; the encoder timed on the 4096-token prefill of every sequence."""
+    import numpy as np
+    import torch
+    import exactkv_amd as exactkv
+    from exactkv_amd import kernels, synthetic
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, TS, Hq, Hkv = 32, 4096, 32, 8
+    lens = np.random.Generator(np.random.PCG64(300)).integers(3500, TS + 1, B)
+    print("[c3] generating data", file=sys.stderr, flush=True)
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=100, device=dev, raw_row_rate=6e-3)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=101, device=dev, raw_row_rate=6e-3)
+    q = synthetic.make_q(B, Hq, seed=102, device=dev)
+    enc = encoder_gbps(exactkv, kernels, k, TS, a.steps, a.warmup)
+    print("[c3] encoder timed", file=sys.stderr, flush=True)
+    kcs, vcs, kbs, vbs, grows = [], [], [], [], []
+    for i in range(a.copies):
+        kc, vc = exactkv.CompressedKV(B, TS, Hkv, 128, reserve=1e-4), exactkv.CompressedKV(B, TS, Hkv, 128, reserve=1e-4)
+        for b in range(B):
+            kc.prefill_slot(b, k[b:b + 1])
+            vc.prefill_slot(b, v[b:b + 1])
+        grows.append(kc.grows + vc.grows)
+        kcs.append(kc)
+        vcs.append(vc)
+        kbs.append(k.clone())
+        vbs.append(v.clone())
+    del k, v
+    torch.cuda.synchronize()
+    print("[c3] caches encoded", file=sys.stderr, flush=True)
+    ld = torch.tensor(lens, dtype=torch.int32, device=dev)
+    ns, sl = kernels.plan_splits(B, Hkv, Hq, TS)
+    out = torch.empty_like(q)
+    o_c = kernels.attention_compressed(q, kcs[0], vcs[0], TS, lens=ld, nsplit=ns, split_len=sl)
+    o_r = kernels.attention_reference(q, kbs[0], vbs[0], TS, lens=ld, nsplit=ns, split_len=sl)
+    identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
+    ms_c = time_loop(lambda i: kernels.attention_compressed(q, kcs[i], vcs[i], TS, lens=ld, nsplit=ns, split_len=sl,
+                                                            out=out), a.steps, a.warmup, a.copies)
+    ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], TS, lens=ld, nsplit=ns, split_len=sl,
+                                                           out=out), a.steps, a.warmup, a.copies)
+    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], TS, ns, sl, True, ld), a.steps, a.warmup,
+                         a.copies)
+    alg = algorithmic_bytes([kcs[0], vcs[0]], B, TS, Hq, Hkv, lens)
+    gbps = alg / (ms_split * 1e-3) / 1e9
+    res = {
+        "metric": "c3 decode-attn us with per-sequence lengths; encoder GB/s", "value": round(ms_c * 1e3, 2),
+        "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_c, 5),
+        "higher_is_better": False, "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "c3: Qwen3-8B shape 32q/8kv, B32 x 4096, lengths U[3500,4096], 0.6% outlier rows",
+                   "B": B, "TS": TS, "Hq": Hq, "Hkv": Hkv, "lens_min": int(lens.min()), "lens_max": int(lens.max()),
+                   "nsplit": ns, "split_len": sl, "cache_copies": a.copies},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
+                     "kernel_us": round(ms_split * 1e3, 2)},
+        "bf16_twin_us": round(ms_b * 1e3, 2), "speedup_vs_bf16": round(ms_b / ms_c, 3),
+        "bit_identical_to_bf16": bool(identical), "pool_grows_in_prefill": grows[0],
+        "raw_rows": int(kcs[0].cnt.item()) + int(vcs[0].cnt.item()), "encoder_GBps": enc,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(res), flush=True)
+
+
 E2E_CONFIG = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                   num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
                   rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=False)
@@ -375,21 +446,22 @@ def e2e(a):
     print(json.dumps(res), flush=True)
 
 
-def split_only(kernels, q, kc, vc, T, ns, sl, compressed):
+def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None):
     """Launch only the split kernel (the dominant kernel) into the shared workspace."""
     from exactkv_amd import _lib
     B, Hq, D = q.shape
     wo, wm, wl = kernels._workspace(q.device, B * Hq, ns)
     scale = D ** -0.5 * kernels.LOG2E
+    lp, lstride = (lens.data_ptr(), lens.stride(0)) if lens is not None else (None, 0)
     if compressed:
         ka, TS, Hkv, _ = kernels._cache_args(kc)
         va, _, _, _ = kernels._cache_args(vc)
         _lib.call("exkv_attn_split_compressed", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, None, 0, ns, sl, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, scale, _lib.stream())
     else:
         TS, Hkv = kc.shape[1], kc.shape[2]
         _lib.call("exkv_attn_split_bf16", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, None, 0, ns, sl, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, scale, _lib.stream())
 
 
 def encoder_gbps(exactkv, kernels, x, T, steps, warmup):

@@ -645,13 +645,12 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         // ---- online softmax: lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
         // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into
         // the exponent's fma: p = 2^(s * scale - m).
-        float sc[4] = {sa[0], sa[1], sa[2], sa[3]};
-        if (ragged) {
-            keep_branch();
+        // Branch-free on purpose: with an opaque-asm branch between the MFMA and these reads,
+        // the compiler's hazard tracking has counted the asm as wait states and let the
+        // reads see the accumulators before the MFMA wrote them.
+        float sc[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (t0 + 4 * g + i >= end) sc[i] = -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i) sc[i] = t0 + 4 * g + i < end ? sa[i] : -INFINITY;
         float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mloc = group_max(mloc) * a.qk_scale;
         const float m_new = fmaxf(m_i, mloc);
@@ -682,6 +681,9 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     }
 
     // ---- merge the page phases of each head (same algebra as the split merge)
+    // the accumulators were last written by MFMAs, possibly across inline assembly that the
+    // hazard tracking may count as wait states: pad explicitly before the first reads
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     const float l_t = group_sum(l_i);
     const int gh = min(16, a.G - hg * 16);
     const int64_t hq0 = (int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16;     // first query head of this wave

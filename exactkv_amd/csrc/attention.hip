@@ -642,6 +642,11 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
         }
 
+        // The score MFMAs' result is read below after the branches above, whose opaque asm the
+        // compiler's hazard tracking has counted as wait states (reads then saw stale
+        // accumulators). Pass it through 16 explicit wait states instead: the asm defines sa,
+        // so every later read follows it.
+        asm volatile("s_nop 7\n\ts_nop 7" : "+v"(sa));
         // ---- online softmax: lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
         // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into
         // the exponent's fma: p = 2^(s * scale - m).

@@ -45,7 +45,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kFusedMaxSplits = 4;   // up to this many splits the split kernel merges in its tail
-constexpr int kDmaPerPage[2] = {8, 7}; // direct-to-LDS loads per page: bf16, compressed
+constexpr int kDmaPerPage[2] = {8, 8}; // direct-to-LDS loads per page: bf16, compressed (raw row included)
 
 // compressed page stage (bytes): K sm 16x128 | K code 16x64 | V sm | V code | K base,
 // V base (128 each); rowmask/rowoff come through the scalar cache instead
@@ -275,23 +275,15 @@ __device__ inline DmaLane dma_lane_offsets(int lane, int64_t rs) {
 }
 
 // Issue one page's kDmaPerPage loads into stage st. row0: row index of the page's token 0
-// ((b*TS + 16*pg)*Hkv + hk); page: its page index.
+// ((b*TS + 16*pg)*Hkv + hk); page: its page index. The compressed page's raw-row load comes
+// last and is always issued (one lane, 16 bytes of the pool's first row, when the page has
+// none in the ring), so every page is the same number of loads and only the raw load waits
+// for the page's rowmask / rowoff.
 template <bool COMP>
 __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row0, int64_t page, uint32_t st,
                                 int lane, const PageMeta& m, uint32_t raw_st, const PairSrc& basep,
                                 const PairSrc& rawp, const PairSrc& rawn) {
     if constexpr (COMP) {
-        // raw rows of the page (K rows in token order, then V rows): entry e = lane / 16 of
-        // at most kRawRing, 16 bytes per lane; pool index = rowoff + rank of the row
-        if (raw_in_ring(m)) {
-            const int nk = __builtin_popcount(m.mk), n = nk + __builtin_popcount(m.mv), e = lane >> 4;
-            const bool isv = e >= nk;
-            int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
-            const int64_t rows = (int64_t)rawn.pick(isv);
-            idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
-            const uint64_t rb = rawp.pick(isv);
-            if (lane < 16 * n) dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
-        }
         const uint8_t* ksm = a.k.sm + row0 * 128;
         const uint8_t* vsm = a.v.sm + row0 * 128;
         dma16(ksm + o.sm0, st + CS_KSM);
@@ -303,6 +295,17 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
         // base rows: lanes 0-7 K, 8-15 V
         const uint64_t bsrc = basep.pick((lane & 8) != 0) + (uint64_t)page * 128 + o.base;
         if (lane < 16) dma16((const void*)(uintptr_t)bsrc, st + CS_BASE);
+        // raw rows of the page (K rows in token order, then V rows): entry e = lane / 16 of
+        // at most kRawRing, 16 bytes per lane; pool index = rowoff + rank of the row
+        const int nk = __builtin_popcount(m.mk);
+        const int n = raw_in_ring(m) ? nk + __builtin_popcount(m.mv) : 0, e = lane >> 4;
+        const bool isv = e >= nk;
+        int64_t idx = n == 0 ? 0 : (isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e);
+        const int64_t rows = (int64_t)rawn.pick(isv);
+        idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+        const uint64_t rb = rawp.pick(isv);
+        if (lane < (n == 0 ? 1 : 16 * n))
+            dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
     } else {
         const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.kb) + row0 * 256;
         const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.vb) + row0 * 256;
@@ -311,6 +314,18 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
             dma16(kp + o.bf_k[j], st + BS_K + j * 1024);
             dma16(vp + o.bf_v[j], st + BS_V + j * 1024);
         }
+    }
+}
+
+// q through LDS: the wavefront's query heads hg*16 .. hg*16 + gh - 1 of KV head hk, head h
+// at qst + 256 h, by direct-to-LDS loads (load d: heads 4d .. 4d + 3) that are waited for
+// like the page loads, so that waiting for q does not also wait for the first pages.
+__device__ inline void q_dma(const AttnArgs& a, int b, int hk, int hg, int gh, int lane, uint32_t qst) {
+    const int nq = (gh + 3) >> 2;
+    for (int d = 0; d < nq; ++d) {
+        const int h = min(4 * d + (lane >> 4), gh - 1);
+        dma16(a.q + ((int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16 + h) * kD + 8 * (lane & 15),
+              qst + (uint32_t)(1024 * d));
     }
 }
 
@@ -447,21 +462,6 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     const int end = min(start + a.split_len, len);
     const int NP = a.TS / kPage;
 
-    // Q^T as the B operand: column = head hg*16 + r of this KV head's group, k-block kc
-    // holds channels 16g + 8kc.. (kc < 2) or 64 + 16g + 8(kc-2).. (kc >= 2).
-    const int hl = hg * 16 + r;
-    uint32_t qw[16];
-    {
-        const uint16_t* qp = a.q + ((int64_t)b * a.Hq + (int64_t)hk * a.G + min(hl, a.G - 1)) * kD;
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            const int d0 = kc < 2 ? 16 * g + 8 * kc : 64 + 16 * g + 8 * (kc - 2);
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (hl < a.G) v = *reinterpret_cast<const u32x4*>(qp + d0);
-            qw[4 * kc] = v.x; qw[4 * kc + 1] = v.y; qw[4 * kc + 2] = v.z; qw[4 * kc + 3] = v.w;
-        }
-    }
-
     float m_i = -INFINITY, l_i = 0.f;
     f32x4 acc[8];
 #pragma unroll
@@ -505,22 +505,39 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         const int64_t page = ((int64_t)b * NP + pg) * rs + hk;
         dma_page<COMP>(a, dl, row0, page, sb, lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), basep, rawp, rawn);
     };
+    // q through the last stage, which no page uses before page NST - 1 is issued
+    const int gh = min(16, a.G - hg * 16);
+    const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
+    q_dma(a, b, hk, hg, gh, lane, qst);
     if (npw > 0) issue(0, ring, m0);
     if (NST == 3 && npw > 1) issue(1, ring + STB, m1);
-    settle(qw);                                        // q (and the first pages) arrive here
+    // q has landed once only the first pages' loads are in flight
+    const int first = min(npw, NST - 1);
+    if (first >= 2)
+        wait_vm<2 * kDmaPerPage[COMP]>();
+    else if (first == 1)
+        wait_vm<kDmaPerPage[COMP]>();
+    else
+        wait_vm<0>();
+    // Q^T as the B operand: column = head hg*16 + r of this KV head's group, k-block kc
+    // holds channels 16g + 8kc.. (kc < 2) or 64 + 16g + 8(kc-2).. (kc >= 2); heads past
+    // the group are zero.
     bf16x8 qop[4];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) qop[kc] = as_bf16x8(qw[4 * kc], qw[4 * kc + 1], qw[4 * kc + 2], qw[4 * kc + 3]);
+    for (int kc = 0; kc < 4; ++kc) {
+        const int d0 = kc < 2 ? 16 * g + 8 * kc : 64 + 16 * g + 8 * (kc - 2);
+        uint4 v = lds16(lds_ptr(qst + (uint32_t)(r * 256 + 2 * d0)));
+        if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
+        qop[kc] = as_bf16x8(v.x, v.y, v.z, v.w);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q is in registers before its stage is reused
 
     progress[wave] = 0;
     int stg = 0;                                       // stage of page j (j % NST)
     for (int j = 0; j < npw; ++j) {
         // stage j is complete once only page j + 1's loads are in flight
         if (NST == 3 && j + 1 < npw) {
-            if (COMP && raw_in_ring(m1))
-                wait_vm<kDmaPerPage[COMP] + 1>();
-            else
-                wait_vm<kDmaPerPage[COMP]>();
+            wait_vm<kDmaPerPage[COMP]>();
         } else {
             wait_vm<0>();
         }
@@ -690,7 +707,6 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     // hazard tracking may count as wait states: pad explicitly before the first reads
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     const float l_t = group_sum(l_i);
-    const int gh = min(16, a.G - hg * 16);
     const int64_t hq0 = (int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16;     // first query head of this wave
     if (nphase == 1) {                                 // one wavefront per head: write its partial
         if (r < gh) {

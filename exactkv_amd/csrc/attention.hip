@@ -407,6 +407,29 @@ __device__ inline void lds_raw_values(uint32_t slot, int q, int g, uint32_t out[
     out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
 }
 
+// Splice the page's raw K (V = false) or V rows into the lane's rebuilt row (lane = token
+// r): from the page's raw slot when they came through the ring (entry = rank of the row,
+// K rows first), else straight from the pool (rare; this waits for every load in flight).
+template <bool V>
+__device__ inline void splice_raw(const AttnArgs& a, const PageMeta& m, uint32_t slot, int r, int g,
+                                  uint32_t d[16]) {
+    const uint32_t mask = V ? m.mv : m.mk;
+    const uint32_t below = (1u << r) - 1u;
+    uint32_t x[16];
+    if (raw_in_ring(m)) {
+        const int e = (V ? __builtin_popcount(m.mk) : 0) + __builtin_popcount(mask & below);
+        lds_raw_values(slot, min(e, kRawRing - 1), g, x);
+    } else {
+        const CSrc& c = V ? a.v : a.k;
+        load_raw_values(c.raw, raw_slot(mask, V ? m.ov : m.ok, r, c.raw_rows), g, x);
+        wait_vm<0>();
+        settle(x);
+    }
+    const bool take = ((mask >> r) & 1u) != 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = take ? x[i] : d[i];
+}
+
 // V tile row r (32 values of the lane) at the tile offset toff of the stage
 __device__ inline void write_v_tile(uint32_t sb, const LdsLane& o, int toff, const uint32_t v[16]) {
     lds_u8* p = lds_ptr(sb + o.tw) + toff;
@@ -550,32 +573,18 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         const bool row_valid = t0 + r < end;
         const PageMeta mc = m0;
 
-        uint32_t kraw[16], vraw[16];
-        if (COMP && (mc.mk | mc.mv) != 0) {
-            if (raw_in_ring(mc)) {
-                // the page's raw rows came with it: entry of token r = its rank among the
-                // page's raw K rows (then V rows)
-                const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
-                const uint32_t below = (1u << r) - 1u;
-                if ((mc.mk >> r) & 1u) lds_raw_values(slot, __builtin_popcount(mc.mk & below), g, kraw);
-                if ((mc.mv >> r) & 1u)
-                    lds_raw_values(slot, __builtin_popcount(mc.mk) + __builtin_popcount(mc.mv & below), g, vraw);
-            } else {
-                // more raw rows than the ring slot holds (rare): fetch them now and wait, before
-                // the next page's loads go out, so the fixed wait counts stay exact
-                if ((mc.mk >> r) & 1u) load_raw_values(a.k.raw, raw_slot(mc.mk, mc.ok, r, a.k.raw_rows), g, kraw);
-                if ((mc.mv >> r) & 1u) load_raw_values(a.v.raw, raw_slot(mc.mv, mc.ov, r, a.v.raw_rows), g, vraw);
-                wait_vm<0>();
-                settle(kraw);
-                settle(vraw);
+        // The next page's loads: the bf16 twin's at once; the compressed cache's once this
+        // page's raw rows are out of their slot, which page j + 2's raw rows reuse.
+        const PageMeta mn = NST == 3 ? m2 : m1;
+        auto issue_next = [&]() {
+            if (j + NST - 1 < npw) {
+                // the recycled stage and raw slot were last read by this wavefront's LDS
+                // accesses: let them finish before the DMA can land there
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(j + NST - 1, ring + (uint32_t)(stn * STB), mn);
             }
-        }
-        if (j + NST - 1 < npw) {
-            // the recycled stage and raw slot were last read by this wavefront's LDS accesses
-            // of this or the previous page: let them finish before the DMA can land there
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(j + NST - 1, ring + (uint32_t)(stn * STB), NST == 3 ? m2 : m1);
-        }
+        };
+        if (!COMP) issue_next();
         if constexpr (COMP) {
             m0 = m1;
             m1 = m2;
@@ -600,13 +609,11 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             PageBytes pk, pv;
             stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
             stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
+            const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
             rebuild_values(pk, kd);
             if (mc.mk != 0) {                          // page with raw K rows
                 keep_branch();
-                if ((mc.mk >> r) & 1u) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) kd[i] = kraw[i];
-                }
+                splice_raw<false>(a, mc, slot, r, g, kd);
             }
             if (ragged) {                              // rows past the end of the split: zero
                 keep_branch();
@@ -623,10 +630,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             rebuild_values(pv, vd);
             if (mc.mv != 0) {
                 keep_branch();
-                if ((mc.mv >> r) & 1u) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) vd[i] = vraw[i];
-                }
+                splice_raw<true>(a, mc, slot, r, g, vd);
             }
             if (ragged) {
                 keep_branch();
@@ -636,6 +640,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
                 }
             }
             write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
+            issue_next();
         } else {
             stage_bf16_k(sb, lo, kd);
             if (ragged) {

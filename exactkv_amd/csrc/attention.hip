@@ -205,6 +205,10 @@ __device__ inline uint32_t lds_addr(const uint8_t* p) {
 __device__ inline void dma16(const void* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
+// 4-byte variant: lane L's dword lands at M0 + 4L.
+__device__ inline void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
 
 // Mark registers as defined here (an empty asm that reads and writes them): the compiler
 // then waits for their loads at this point, once, instead of at every later use inside
@@ -505,9 +509,13 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     const PairSrc rawp = pair_src((uint64_t)(uintptr_t)a.k.raw, (uint64_t)(uintptr_t)a.v.raw);
     const PairSrc rawn = pair_src((uint64_t)a.k.raw_rows, (uint64_t)a.v.raw_rows);
 
-    // rowmask / rowoff: scalar loads (constant address space: read-only through the scalar
-    // cache, counted by lgkmcnt), three pages ahead of their page's compute
-    auto meta = [&](int j) {
+    // rowmask / rowoff of the wavefront's pages. Lane i holds page i's (i < 64): loaded once,
+    // with q, by direct-to-LDS loads, then read into VGPRs, so that a page's values are
+    // v_readlane of its index. Scalar loads inside the loop would cost more: SMEM and LDS
+    // share lgkmcnt and SMEM returns out of order, so every wait for an LDS read there would
+    // also wait for the scalar loads in flight. Scalar loads serve the first two pages (their
+    // raw rows go out with the first DMA) and pages past 64.
+    auto meta_s = [&](int j) {
         PageMeta m{0u, 0u, 0, 0};
         if constexpr (COMP) {
             const int64_t page = ((int64_t)b * NP + p0 + phase + nphase * j) * rs + hk;
@@ -518,10 +526,16 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         }
         return m;
     };
-    PageMeta m0{0u, 0u, 0, 0}, m1{0u, 0u, 0, 0}, m2{0u, 0u, 0, 0};   // pages j, j + 1, j + 2
-    if (COMP && npw > 0) m0 = meta(0);
-    if (COMP && npw > 1) m1 = meta(1);
-    if (COMP && npw > 2) m2 = meta(2);
+    uint32_t vmk = 0u, vmv = 0u;
+    int32_t vok = 0, vov = 0;
+    auto meta = [&](int j) {
+        if (j >= 64) return meta_s(j);
+        return PageMeta{(uint32_t)__builtin_amdgcn_readlane((int)vmk, j), (uint32_t)__builtin_amdgcn_readlane((int)vmv, j),
+                        __builtin_amdgcn_readlane(vok, j), __builtin_amdgcn_readlane(vov, j)};
+    };
+    PageMeta m0{0u, 0u, 0, 0}, m1{0u, 0u, 0, 0};
+    if (COMP && npw > 0) m0 = meta_s(0);
+    if (COMP && npw > 1) m1 = meta_s(1);
     auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
         const int pg = p0 + phase + nphase * j;
         const int64_t row0 = ((int64_t)b * a.TS + (int64_t)pg * kPage) * rs + hk;
@@ -532,6 +546,15 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     const int gh = min(16, a.G - hg * 16);
     const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
     q_dma(a, b, hk, hg, gh, lane, qst);
+    const uint32_t mst = qst + 4096u;                  // rowmask K | rowoff K | rowmask V | rowoff V
+    if constexpr (COMP) {
+        const int pg = min(p0 + phase + nphase * min(lane, max(npw - 1, 0)), NP - 1);
+        const int64_t page = ((int64_t)b * NP + pg) * rs + hk;
+        dma4(a.k.rowmask + page, mst);
+        dma4(a.k.rowoff + page, mst + 256u);
+        dma4(a.v.rowmask + page, mst + 512u);
+        dma4(a.v.rowoff + page, mst + 768u);
+    }
     if (npw > 0) issue(0, ring, m0);
     if (NST == 3 && npw > 1) issue(1, ring + STB, m1);
     // q has landed once only the first pages' loads are in flight
@@ -553,7 +576,13 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
         qop[kc] = as_bf16x8(v.x, v.y, v.z, v.w);
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q is in registers before its stage is reused
+    if constexpr (COMP) {
+        vmk = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 4u * lane));
+        vok = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 256u + 4u * lane));
+        vmv = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 512u + 4u * lane));
+        vov = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 768u + 4u * lane));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers before their stage is reused
 
     progress[wave] = 0;
     int stg = 0;                                       // stage of page j (j % NST)
@@ -571,11 +600,11 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         const int t0 = pg * kPage;
         const bool ragged = t0 + kPage > end;          // uniform: only the last page of a split
         const bool row_valid = t0 + r < end;
-        const PageMeta mc = m0;
+        const PageMeta mc = COMP ? meta(j) : PageMeta{0u, 0u, 0, 0};
 
         // The next page's loads: the bf16 twin's at once; the compressed cache's once this
         // page's raw rows are out of their slot, which page j + 2's raw rows reuse.
-        const PageMeta mn = NST == 3 ? m2 : m1;
+        const PageMeta mn = COMP && j + NST - 1 < npw ? meta(j + NST - 1) : PageMeta{0u, 0u, 0, 0};
         auto issue_next = [&]() {
             if (j + NST - 1 < npw) {
                 // the recycled stage and raw slot were last read by this wavefront's LDS
@@ -585,11 +614,6 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
         };
         if (!COMP) issue_next();
-        if constexpr (COMP) {
-            m0 = m1;
-            m1 = m2;
-            if (j + 3 < npw) m2 = meta(j + 3);
-        }
         // Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one, and
         // the older one's first loads are also served first: left alone it runs ahead and its
         // partner finishes last. The one that is behind takes the higher priority.

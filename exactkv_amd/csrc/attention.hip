@@ -789,12 +789,47 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     merge_tail(a, b, hb, hg, gh, split);
 }
 
-// Separate merge of the split partials, one wavefront per (sequence, query head) row.
-__global__ void __launch_bounds__(64) attn_reduce_kernel(const float* po, const float* pm, const float* pl,
-                                                         uint16_t* out, int ns) {
+// Separate merge of the split partials, one workgroup per (sequence, query head) row.
+// Up to 32 splits: one wavefront, every load of the row in flight at once (the fused
+// merge's code, so both give the same bits). More: kReduceWaves wavefronts each take a
+// contiguous range of splits (one round trip per 32 of them) under the common M, and
+// wavefront 0 adds their sums in wavefront order.
+constexpr int kReduceWaves = 8;
+__global__ void __launch_bounds__(64 * kReduceWaves) attn_reduce_kernel(const float* po, const float* pm,
+                                                                        const float* pl, uint16_t* out, int ns) {
     const int64_t row = blockIdx.x;
-    reinterpret_cast<uint32_t*>(out + row * kD)[threadIdx.x] =
-        merge_row(po + row * ns * kD, pm + row * ns, pl + row * ns, ns, threadIdx.x);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const float* o = po + row * ns * kD;
+    const float* m = pm + row * ns;
+    const float* l = pl + row * ns;
+    if (nw == 1) {
+        reinterpret_cast<uint32_t*>(out + row * kD)[lane] = merge_row(o, m, l, ns, lane);
+        return;
+    }
+    float mm = -INFINITY;
+    for (int s = lane; s < ns; s += 64) mm = fmaxf(mm, m[s]);
+    const float M = wave_max(mm);
+    const int per = (ns + nw - 1) / nw, c0 = min(ns, wave * per), c1 = min(ns, c0 + per);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+    for (int c = c0; c < c1; c += 32) {
+        const int n = c1 - c < 32 ? c1 - c : 32;
+        const float ws = lane < n ? fast_exp2(m[c + lane] - M) : 0.f;
+        const float ls = lane < n ? l[c + lane] : 0.f;
+        merge_chunk(reinterpret_cast<const float2*>(o), c, n, ws, ls, lane, n0, n1, den);
+    }
+    __shared__ float part[kReduceWaves][3][64];
+    part[wave][0][lane] = n0;
+    part[wave][1][lane] = n1;
+    part[wave][2][lane] = den;
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < nw; ++w) {
+            n0 += part[w][0][lane];
+            n1 += part[w][1][lane];
+            den += part[w][2][lane];
+        }
+        reinterpret_cast<uint32_t*>(out + row * kD)[lane] = pack_bf16x2(n0 / den, n1 / den);
+    }
 }
 
 }  // namespace exkv
@@ -844,7 +879,8 @@ static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
 
 static int launch_reduce(const float* o, const float* m, const float* l, void* out, int64_t rows, int ns,
                          hipStream_t stream) {
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rows), dim3(64), 0, stream, o, m, l, (uint16_t*)out, ns);
+    const unsigned threads = ns <= 32 ? 64u : 64u * (unsigned)min(kReduceWaves, (ns + 31) / 32);
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rows), dim3(threads), 0, stream, o, m, l, (uint16_t*)out, ns);
     return hip_status(hipGetLastError(), "attn_reduce");
 }
 

@@ -64,9 +64,10 @@ def merge_units(B, Hkv, Hq):
 
 
 FUSED_MERGE_MAX_SPLITS = 4   # up to this many splits the split kernel's last workgroup can merge
-FUSED_MERGE_MAX_BLOCKS = 256  # ... and only within one round of workgroups: the merging workgroup's
-#                               device-scope fences write back its L2, which costs more than the
-#                               separate merge launch once many workgroups do it
+# The fused merge is available (fused_merge=True) but not the default: every workgroup's
+# device-scope release writes back its XCD's L2, and measured on MI355X that costs more
+# than the separate merge launch at every grid size tried (16 workgroups: +5 us, 64: +14 us,
+# 256: +78 us per call).
 
 
 def _counters(dev, units):
@@ -77,12 +78,11 @@ def _counters(dev, units):
     return c
 
 
-def _fused_counters(dev, B, Hkv, Hq, ns):
+def _fused_counters(dev, B, Hkv, Hq, ns, fused_merge):
     """Arrival counters when the merge runs in the split kernel's tail, else None."""
-    units = merge_units(B, Hkv, Hq)
-    if ns > FUSED_MERGE_MAX_SPLITS or units * ns > FUSED_MERGE_MAX_BLOCKS:
+    if not fused_merge or ns > FUSED_MERGE_MAX_SPLITS:
         return None
-    return _counters(dev, units)
+    return _counters(dev, merge_units(B, Hkv, Hq))
 
 
 def _check_q(q):
@@ -129,7 +129,7 @@ def _lens_arg(lens, B):
 
 
 def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                         split_len=None, out=None):
+                         split_len=None, out=None, fused_merge=False):
     """q [B, Hq, 128] bf16 contiguous; kc, vc: CompressedKV objects (or their .buffers()
     dicts); T: valid tokens. Returns bf16 [B, Hq, 128], bit-identical to
     attention_reference on the same contents and split plan."""
@@ -142,7 +142,7 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
-    cnt = _fused_counters(q.device, B, Hkv, Hq, ns)
+    cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
               cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
@@ -151,7 +151,7 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
 
 
 def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                        split_len=None, out=None):
+                        split_len=None, out=None, fused_merge=False):
     """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous)."""
     _check_q(q)
     if k.shape != v.shape or k.dim() != 4 or k.dtype != torch.bfloat16 or not (k.is_contiguous() and v.is_contiguous()):
@@ -163,7 +163,7 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
-    cnt = _fused_counters(q.device, B, Hkv, Hq, ns)
+    cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
               wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl,

@@ -71,7 +71,7 @@ def test_attention_bit_identical_and_accurate(B, T, Hq, Hkv):
     assert np.abs(o_c.double().cpu().numpy() - r64).max() < 2e-2       # the reference test's bound
 
 
-@pytest.mark.parametrize("ns_sl", [(1, None), (None, 32), (None, 64), (None, 96)])
+@pytest.mark.parametrize("ns_sl", [(1, None), (None, 16), (None, 32), (None, 64), (None, 96)])   # 16: 63 splits, multi-wavefront merge
 def test_split_plans(ns_sl):
     B, T, Hq, Hkv = 2, 1000, 32, 8
     q, k, v = _ref_case(B, T, Hq, Hkv, seed=5)
@@ -86,6 +86,10 @@ def test_split_plans(ns_sl):
     o_r = kernels.attention_reference(qd, kd, vd, T, nsplit=ns, split_len=sl)
     assert same_bits(o_c, o_r)
     assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+    if ns <= kernels.FUSED_MERGE_MAX_SPLITS:           # the merge in the split kernel's tail: same bits
+        for _ in range(2):                             # the arrival counters reset for the next call
+            assert same_bits(kernels.attention_compressed(qd, kc, vc, T, nsplit=ns, split_len=sl, fused_merge=True), o_c)
+            assert same_bits(kernels.attention_reference(qd, kd, vd, T, nsplit=ns, split_len=sl, fused_merge=True), o_r)
 
 
 def test_synthetic_keys_with_raw_rows_and_zero_groups():

@@ -31,15 +31,16 @@ extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 // Split plan for MI355X: about target_blocks workgroups in total over B * (Hkv / HW) * head
 // groups, where a workgroup covers HW = gcd(Hkv, 8) KV heads -- 256 by default, one per
 // CU, since a workgroup holds ~150 KB of LDS -- with
-// at least min_split tokens per split (so each of a workgroup's 8 wavefronts streams
-// whole 16-token pages) and a split length that is a multiple of 32. Plays the role of the reference's choose_split
+// at least min_split tokens per split (64 by default: a wavefront's pages follow one
+// another at about one memory round trip each, so a few units are served best by many
+// short splits) and a split length that is a multiple of 32. Plays the role of the reference's choose_split
 // (kernels.py:273-277), which targets 512 programs for a 128-SM-class GPU.
 extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                                 int32_t min_split, int32_t* nsplit, int32_t* split_len) {
     EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits: bad arguments");
     EXKV_REQUIRE(nsplit && split_len, "plan_splits: null output");
     if (target_blocks <= 0) target_blocks = 256;
-    if (min_split <= 0) min_split = 256;
+    if (min_split <= 0) min_split = 64;
     const int64_t hg = (Hq / Hkv + 15) / 16;
     int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8)
     while (m) {

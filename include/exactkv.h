@@ -121,7 +121,7 @@ int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, vo
                      int32_t nsplit, int32_t D, hipStream_t stream);
 
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
- * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 256), split_len a multiple of 32.
+ * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 64), split_len a multiple of 32.
  * Replaces: kernels.py:273-277 choose_split. */
 int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);

@@ -47,11 +47,11 @@ def test_argument_errors_are_reported_without_launching():
 @pytest.mark.parametrize("B,Hkv,Hq,T,expect", [
     (8, 8, 32, 8192, (32, 256)),       # a workgroup covers all 8 KV heads: 8 units x 32 splits = 256
     (1, 8, 32, 131072, (256, 512)),
-    (1, 4, 28, 32768, (128, 256)),     # 4 KV heads per workgroup; capped by min_split 256
+    (1, 4, 28, 32768, (256, 128)),     # 4 KV heads per workgroup: one unit, 256 splits
     (32, 8, 32, 4096, (8, 512)),
-    (1, 4, 28, 8000, (32, 256)),
+    (1, 4, 28, 8000, (125, 64)),       # capped by min_split 64
     (4, 2, 16, 17, (1, 32)),
-    (2, 2, 64, 1000, (4, 256)),        # G = 32: two head groups per KV head
+    (2, 2, 64, 1000, (16, 64)),        # G = 32: two head groups per KV head
     (620, 8, 32, 4352, (4, 1088)),     # more units than one round: about 8 rounds (2480 workgroups)
     (256, 8, 32, 4096, (8, 512)),
     (255, 8, 32, 4096, (2, 2048)),     # still one round of units: two splits reach 256 blocks

@@ -52,8 +52,9 @@ def test_argument_errors_are_reported_without_launching():
     (1, 4, 28, 8000, (125, 64)),       # capped by min_split 64
     (4, 2, 16, 17, (1, 32)),
     (2, 2, 64, 1000, (16, 64)),        # G = 32: two head groups per KV head
-    (620, 8, 32, 4352, (4, 1088)),     # more units than one round: about 8 rounds (2480 workgroups)
-    (256, 8, 32, 4096, (8, 512)),
+    (620, 8, 32, 4352, (2, 2176)),     # more units than one round: >= 2 rounds, the last >= 95% full (4.84 rounds)
+    (256, 8, 32, 4096, (2, 2048)),     # exactly two rounds
+    (300, 8, 32, 4096, (5, 832)),      # 5.86 rounds: the first split count whose last round is >= 95% full
     (255, 8, 32, 4096, (2, 2048)),     # still one round of units: two splits reach 256 blocks
 ])
 def test_plan_splits(B, Hkv, Hq, T, expect):

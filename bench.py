@@ -166,7 +166,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e"])
+    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -181,11 +181,11 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload in ("e2e", "c3"):
+    if a.workload in ("e2e", "c3", "c2a_paged"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
-        return e2e(a) if a.workload == "e2e" else c3_stress(a)
+        return e2e(a) if a.workload == "e2e" else c3_stress(a) if a.workload == "c3" else paged_c2a(a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -273,6 +273,71 @@ def main():
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, min(a.cpu_seqs, B), a.cpu_seconds)
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
+    print(json.dumps(res), flush=True)
+
+
+def paged_c2a(a):
+    """c2a over paged caches: the 8 x 8192 tokens as 4096 pages scattered at random over a
+    pool of 4160 pages (one 66,560-token sequence per array), block table [8, 512]."""
+    import numpy as np
+    import torch
+    import exactkv_amd as exactkv
+    from exactkv_amd import kernels, synthetic
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, T, Hq, Hkv, POOL = 8, 8192, 32, 8, 4160
+    npg = T // 16
+    print("[paged] generating data", file=sys.stderr, flush=True)
+    q = synthetic.make_q(B, Hq, seed=102, device=dev)
+    kcs, vcs, kbs, vbs, bts = [], [], [], [], []
+    for i in range(a.copies):
+        k = synthetic.make_kv(1, POOL * 16, Hkv, kind="k", seed=300 + i, device=dev)
+        v = synthetic.make_kv(1, POOL * 16, Hkv, kind="v", seed=400 + i, device=dev)
+        kc, vc = exactkv.CompressedKV(1, POOL * 16, Hkv, 128), exactkv.CompressedKV(1, POOL * 16, Hkv, 128)
+        kc.prefill_slot(0, k)
+        vc.prefill_slot(0, v)
+        perm = np.random.Generator(np.random.PCG64(500 + i)).permutation(POOL)[:B * npg]
+        bts.append(torch.tensor(perm.reshape(B, npg), dtype=torch.int32, device=dev))
+        kcs.append(kc)
+        vcs.append(vc)
+        kbs.append(k)
+        vbs.append(v)
+    torch.cuda.synchronize()
+    print("[paged] pools encoded", file=sys.stderr, flush=True)
+    ns, sl = kernels.plan_splits(B, Hkv, Hq, T)
+    out = torch.empty_like(q)
+    o_c = kernels.attention_compressed(q, kcs[0], vcs[0], T, nsplit=ns, split_len=sl, block_table=bts[0])
+    o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl, block_table=bts[0])
+    identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
+    ms_c = time_loop(lambda i: kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl,
+                                                            out=out, block_table=bts[i]), a.steps, a.warmup, a.copies)
+    ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out,
+                                                           block_table=bts[i]), a.steps, a.warmup, a.copies)
+    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True, block_table=bts[i]),
+                         a.steps, a.warmup, a.copies)
+    # algorithmic bytes: those of the gathered pages (the table's pages of the pool)
+    alg = 0
+    for c in (kcs[0], vcs[0]):
+        rm = c.rowmask[0][bts[0].long().flatten()].to(torch.int64)           # [B * npg, Hkv]
+        raw_rows = int(sum(((rm >> bit) & 1).sum().item() for bit in range(16)))
+        alg += B * T * Hkv * 192 + B * npg * Hkv * 136 + raw_rows * 256
+    alg += 2 * B * Hq * 128 * 2
+    gbps = alg / (ms_split * 1e-3) / 1e9
+    res = {
+        "metric": "c2a decode-attn us over paged caches (block tables)", "value": round(ms_c * 1e3, 2), "unit": "us",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_c, 5), "higher_is_better": False,
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "c2a_paged: Llama-3.1-8B decode attention 32q/8kv, B8 x 8192 ctx, pages scattered "
+                               "over a 4160-page pool", "B": B, "T": T, "Hq": Hq, "Hkv": Hkv, "pool_pages": POOL,
+                   "nsplit": ns, "split_len": sl, "cache_copies": a.copies},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "attn_split_kernel<compressed> (paged)", "algorithmic_bytes": alg,
+                     "kernel_us": round(ms_split * 1e3, 2)},
+        "bf16_twin_us": round(ms_b * 1e3, 2), "speedup_vs_bf16": round(ms_b / ms_c, 3),
+        "bit_identical_to_bf16": bool(identical), "gpu": torch.cuda.get_device_name(0),
+    }
     print(json.dumps(res), flush=True)
 
 
@@ -453,13 +518,20 @@ def e2e(a):
     print(json.dumps(res), flush=True)
 
 
-def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None):
+def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table=None):
     """Launch only the split kernel (the dominant kernel) into the shared workspace."""
     from exactkv_amd import _lib
     B, Hq, D = q.shape
     wo, wm, wl = kernels._workspace(q.device, B * Hq, ns)
     scale = D ** -0.5 * kernels.LOG2E
     lp, lstride = (lens.data_ptr(), lens.stride(0)) if lens is not None else (None, 0)
+    if block_table is not None:                        # compressed pool of pages
+        ka, TSp, Hkv, Bp = kernels._cache_args(kc)
+        va, _, _, _ = kernels._cache_args(vc)
+        _lib.call("exkv_attn_split_compressed_paged", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
+                  wl.data_ptr(), block_table.data_ptr(), block_table.shape[1], Bp * TSp // 16, B, Hq, Hkv, D, T,
+                  block_table.shape[1] * 16, lp, lstride, ns, sl, scale, _lib.stream())
+        return
     if compressed:
         ka, TS, Hkv, _ = kernels._cache_args(kc)
         va, _, _, _ = kernels._cache_args(vc)

@@ -29,6 +29,14 @@ SIGNATURES = {
                                    _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
     "exkv_attn_split_bf16": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
                              _f32, _p],
+    "exkv_attn_compressed_paged": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p,
+                                   _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
+                                   _f32, _p],
+    "exkv_attn_split_compressed_paged": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
+                                         _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32,
+                                         _i32, _f32, _p],
+    "exkv_attn_bf16_paged": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                             _p, _i64, _i32, _i32, _f32, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],

@@ -112,6 +112,12 @@ struct AttnArgs {
     float qk_scale;
     uint16_t* out;            // [B, Hq, 128] bf16, written by the last workgroup of each unit
     int32_t* counters;        // [gridDim.y] arrival counters (zero between calls); nullptr: no merge
+    // Paged caches: the arrays hold a pool of pool_pages pages (one sequence of
+    // 16 * pool_pages tokens) and page p of sequence b is pool page block_table[b * bt_stride
+    // + p]. nullptr: page p of sequence b is page b * TS / 16 + p of [B, TS, ...] arrays.
+    const int32_t* block_table;
+    int64_t bt_stride;
+    int pool_pages;
 };
 
 // ---- split merge (kernels.py:33-43): M = max_s m_s, w_s = 2^(m_s - M),
@@ -515,10 +521,20 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     // share lgkmcnt and SMEM returns out of order, so every wait for an LDS read there would
     // also wait for the scalar loads in flight. Scalar loads serve the first two pages (their
     // raw rows go out with the first DMA) and pages past 64.
+    // Page index (in the arrays) of the wavefront's page j: contiguous, or through the block
+    // table, whose entries for the wavefront's pages are read once into VGPRs (lane i: page
+    // i, i < 64) like the page table below.
+    int32_t vbt = 0;
+    auto gpage = [&](int j) -> int64_t {
+        const int lp = p0 + phase + nphase * j;
+        if (a.block_table == nullptr) return (int64_t)b * NP + lp;
+        const int32_t e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(a.block_table + b * a.bt_stride + lp);
+        return (int64_t)min((uint32_t)e, (uint32_t)(a.pool_pages - 1));     // a bad entry cannot read out of bounds
+    };
     auto meta_s = [&](int j) {
         PageMeta m{0u, 0u, 0, 0};
         if constexpr (COMP) {
-            const int64_t page = ((int64_t)b * NP + p0 + phase + nphase * j) * rs + hk;
+            const int64_t page = gpage(j) * rs + hk;
             m.mk = (uint32_t)const_ld(a.k.rowmask + page);
             m.ok = const_ld(a.k.rowoff + page);
             m.mv = (uint32_t)const_ld(a.v.rowmask + page);
@@ -534,22 +550,32 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
                         __builtin_amdgcn_readlane(vok, j), __builtin_amdgcn_readlane(vov, j)};
     };
     PageMeta m0{0u, 0u, 0, 0}, m1{0u, 0u, 0, 0};
-    if (COMP && npw > 0) m0 = meta_s(0);
-    if (COMP && npw > 1) m1 = meta_s(1);
     auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
-        const int pg = p0 + phase + nphase * j;
-        const int64_t row0 = ((int64_t)b * a.TS + (int64_t)pg * kPage) * rs + hk;
-        const int64_t page = ((int64_t)b * NP + pg) * rs + hk;
+        const int64_t gp = gpage(j);
+        const int64_t row0 = gp * kPage * rs + hk;
+        const int64_t page = gp * rs + hk;
         dma_page<COMP>(a, dl, row0, page, sb, lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), basep, rawp, rawn);
     };
     // q through the last stage, which no page uses before page NST - 1 is issued
     const int gh = min(16, a.G - hg * 16);
     const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
-    q_dma(a, b, hk, hg, gh, lane, qst);
     const uint32_t mst = qst + 4096u;                  // rowmask K | rowoff K | rowmask V | rowoff V
+    if (a.block_table != nullptr) {                    // the block-table entries first: every address needs them
+        const uint32_t bst = mst + 1024u;
+        const int lp = p0 + phase + nphase * min(lane, max(npw - 1, 0));
+        dma4(a.block_table + b * a.bt_stride + min(lp, (int)(a.TS / kPage) - 1), bst);
+        wait_vm<0>();
+        vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (COMP && npw > 0) m0 = meta_s(0);
+    if (COMP && npw > 1) m1 = meta_s(1);
+    q_dma(a, b, hk, hg, gh, lane, qst);
     if constexpr (COMP) {
-        const int pg = min(p0 + phase + nphase * min(lane, max(npw - 1, 0)), NP - 1);
-        const int64_t page = ((int64_t)b * NP + pg) * rs + hk;
+        const int i = min(lane, max(npw - 1, 0));     // per lane: the wavefront's page i
+        const int64_t gp = a.block_table == nullptr ? (int64_t)b * NP + min(p0 + phase + nphase * i, NP - 1)
+                                                    : (int64_t)min((uint32_t)vbt, (uint32_t)(a.pool_pages - 1));
+        const int64_t page = gp * rs + hk;
         dma4(a.k.rowmask + page, mst);
         dma4(a.k.rowoff + page, mst + 256u);
         dma4(a.v.rowmask + page, mst + 512u);
@@ -980,6 +1006,63 @@ extern "C" int exkv_attn_split_bf16(const void* q, const void* k, const void* v,
     AttnArgs a;
     const int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
     return rc ? rc : launch_split(false, a, stream);
+}
+
+// Paged caches: the compressed (or bf16) arrays hold pool_pages pages of 16 tokens (shape
+// [1, 16 * pool_pages, Hkv, ...]); page p of sequence b is pool page block_table[b *
+// bt_stride + p] (entries clamped to the pool). TS is the sequences' capacity in tokens
+// (at most 16 * bt_stride).
+static int set_paged(AttnArgs& a, const int32_t* block_table, int64_t bt_stride, int32_t pool_pages, int32_t TS) {
+    EXKV_REQUIRE(block_table, "attention (paged): null block table");
+    EXKV_REQUIRE(pool_pages > 0, "attention (paged): pool_pages=%d", pool_pages);
+    EXKV_REQUIRE(bt_stride > 0 && (int64_t)TS <= 16 * bt_stride,
+                 "attention (paged): TS=%d exceeds the block table's %lld pages", TS, (long long)bt_stride);
+    a.block_table = block_table;
+    a.bt_stride = bt_stride;
+    a.pool_pages = pool_pages;
+    return EXKV_OK;
+}
+
+extern "C" int exkv_attn_compressed_paged(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, const int32_t* block_table,
+                                          int64_t bt_stride, int32_t pool_pages, EXKV_SHAPE_PARAMS,
+                                          hipStream_t stream) {
+    AttnArgs a;
+    int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
+    if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
+    if (rc) return rc;
+    EXKV_REQUIRE(out, "attn_compressed_paged: null output");
+    if (ws_cnt && nsplit <= kFusedMaxSplits) {
+        a.out = (uint16_t*)out;
+        a.counters = ws_cnt;
+        return launch_split(true, a, stream);
+    }
+    rc = launch_split(true, a, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
+}
+
+extern "C" int exkv_attn_split_compressed_paged(EXKV_C_PARAMS, const int32_t* block_table, int64_t bt_stride,
+                                                int32_t pool_pages, EXKV_SHAPE_PARAMS, hipStream_t stream) {
+    AttnArgs a;
+    int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
+    if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
+    return rc ? rc : launch_split(true, a, stream);
+}
+
+extern "C" int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_o, float* ws_m,
+                                    float* ws_l, int32_t* ws_cnt, void* out, const int32_t* block_table,
+                                    int64_t bt_stride, int32_t pool_pages, EXKV_SHAPE_PARAMS, hipStream_t stream) {
+    AttnArgs a;
+    int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
+    if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
+    if (rc) return rc;
+    EXKV_REQUIRE(out, "attn_bf16_paged: null output");
+    if (ws_cnt && nsplit <= kFusedMaxSplits) {
+        a.out = (uint16_t*)out;
+        a.counters = ws_cnt;
+        return launch_split(false, a, stream);
+    }
+    rc = launch_split(false, a, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
 }
 
 extern "C" int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, void* out, int64_t rows,

@@ -130,22 +130,44 @@ def _lens_arg(lens, B):
     return _lib.ptr(lens, align=4, what="lens"), stride
 
 
+def _block_table_arg(block_table, B):
+    """(pointer, stride, capacity in tokens) of a paged call's int32 [B, max_pages] table."""
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous int32 [B, max_pages] tensor")
+    if block_table.shape[0] < B:
+        raise ValueError(f"block_table has {block_table.shape[0]} rows for B={B}")
+    return _lib.ptr(block_table, what="block_table"), block_table.shape[1], block_table.shape[1] * P
+
+
 def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                         split_len=None, out=None, fused_merge=False):
+                         split_len=None, out=None, fused_merge=False, block_table=None):
     """q [B, Hq, 128] bf16 contiguous; kc, vc: CompressedKV objects (or their .buffers()
     dicts); T: valid tokens. Returns bf16 [B, Hq, 128], bit-identical to
-    attention_reference on the same contents and split plan."""
+    attention_reference on the same contents and split plan.
+
+    block_table (int32 [B, max_pages], on the GPU): paged caches. kc / vc are then pools
+    of pages (any [Bp, TSp] shape, read as Bp * TSp / 16 pages in order) and page p of
+    sequence b is pool page block_table[b, p]; T / lens count tokens of the sequences."""
     _check_q(q)
     ka, TS, Hkv, Bc = _cache_args(kc)
     va, TSv, Hv, Bv = _cache_args(vc)
     B, Hq, D = q.shape
-    if (TSv, Hv) != (TS, Hkv) or Bc < B or Bv < B:
+    if (TSv, Hv) != (TS, Hkv) or (Bc < B or Bv < B if block_table is None else Bc != Bv):
         raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
+    if block_table is not None:
+        bt, bts, cap = _block_table_arg(block_table, B)
+        pool_pages = Bc * TS // P
+        TS = cap
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
+    if block_table is not None:
+        _lib.call("exkv_attn_compressed_paged", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
+                  cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B, Hq, Hkv, D,
+                  int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+        return out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
               cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
               _lib.stream())
@@ -153,20 +175,32 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
 
 
 def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                        split_len=None, out=None, fused_merge=False):
-    """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous)."""
+                        split_len=None, out=None, fused_merge=False, block_table=None):
+    """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous);
+    with block_table, k and v are pools of pages as in attention_compressed."""
     _check_q(q)
     if k.shape != v.shape or k.dim() != 4 or k.dtype != torch.bfloat16 or not (k.is_contiguous() and v.is_contiguous()):
         raise ValueError("k and v must be contiguous bf16 [B, TS, Hkv, 128] tensors of one shape")
     B, Hq, D = q.shape
     TS, Hkv = k.shape[1], k.shape[2]
-    if k.shape[0] < B or k.shape[3] != D:
+    if (block_table is None and k.shape[0] < B) or k.shape[3] != D:
         raise ValueError("k/v hold fewer sequences than q or have the wrong head dim")
+    if block_table is not None:
+        if TS % P:
+            raise ValueError(f"a page pool's token count must be a multiple of {P} (got {TS})")
+        bt, bts, cap = _block_table_arg(block_table, B)
+        pool_pages = k.shape[0] * TS // P
+        TS = cap
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
+    if block_table is not None:
+        _lib.call("exkv_attn_bf16_paged", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
+                  wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B,
+                  Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+        return out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
               wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl,
               D ** -0.5 * LOG2E, _lib.stream())

@@ -120,6 +120,37 @@ int exkv_attn_split_bf16(const void* q, const void* k, const void* v, float* ws_
 int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, void* out, int64_t rows,
                      int32_t nsplit, int32_t D, hipStream_t stream);
 
+/* Paged caches (block tables): the arrays hold a pool of pool_pages 16-token pages, laid out
+ * as one sequence ([1, 16*pool_pages, Hkv, ...] and [1, pool_pages, Hkv, ...]), and page p of
+ * sequence b is pool page block_table[b*bt_stride + p] (int32; entries are clamped to the
+ * pool). T / lens / TS count the sequences' tokens (TS <= 16*bt_stride). Same kernels and
+ * bits as the contiguous calls on the same page contents.
+ * No counterpart in the reference, which stores [B, TS, ...] only: this is the first item of
+ * the paged serving layout its README lists as future work (README.md:121-123). */
+int exkv_attn_compressed_paged(const void* q, const void* k_sm, const void* k_code, const void* k_base,
+                               const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
+                               int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
+                               const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
+                               int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, int32_t* ws_cnt,
+                               void* out, const int32_t* block_table, int64_t bt_stride, int32_t pool_pages,
+                               int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                               const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
+                               float qk_scale, hipStream_t stream);
+int exkv_attn_split_compressed_paged(const void* q, const void* k_sm, const void* k_code, const void* k_base,
+                                     const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
+                                     int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
+                                     const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
+                                     int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l,
+                                     const int32_t* block_table, int64_t bt_stride, int32_t pool_pages, int32_t B,
+                                     int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                                     const int32_t* lens, int64_t lens_stride, int32_t nsplit,
+                                     int32_t split_len, float qk_scale, hipStream_t stream);
+int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
+                         int32_t* ws_cnt, void* out, const int32_t* block_table, int64_t bt_stride,
+                         int32_t pool_pages, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
+                         const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
+                         float qk_scale, hipStream_t stream);
+
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
  * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 64), split_len a multiple of 32.
  * Replaces: kernels.py:273-277 choose_split. */

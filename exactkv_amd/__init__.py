@@ -6,6 +6,7 @@ for gfx950 behind the reference's Python API (drop-in for zyfyz666/exactkv's nam
 """
 from .cache import CompressedKV, BF16KV, check_overflow
 from .attention import decode_attention
+from .paged import PageTable, PagedCompressedKV, PagedBF16KV
 from .codec import encode_reference, decode_reference, bits_per_value
 from .kernels import attention_compressed, attention_reference, decode_to_bf16, encode_pages
 
@@ -20,4 +21,5 @@ def __getattr__(name):
 __version__ = "0.1.0"
 __all__ = ["CompressedKV", "BF16KV", "check_overflow", "decode_attention", "Engine",
            "encode_reference", "decode_reference", "bits_per_value",
-           "attention_compressed", "attention_reference", "decode_to_bf16", "encode_pages"]
+           "attention_compressed", "attention_reference", "decode_to_bf16", "encode_pages",
+           "PageTable", "PagedCompressedKV", "PagedBF16KV"]

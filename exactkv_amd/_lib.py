@@ -17,9 +17,14 @@ _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c
 SIGNATURES = {
     "exkv_encode_pages": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_encode_pages_paged": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
+                                _i32, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_cache_append": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                           _i32, _p],
     "exkv_bf16_append": [_p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _p],
+    "exkv_cache_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _i64,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_bf16_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
                              _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],

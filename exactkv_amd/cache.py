@@ -221,7 +221,7 @@ def check_overflow(caches):
     """After a page boundary: one host sync for all compressed caches, then re-encode any
     page that overflowed its raw pool and restore every pool's headroom. Returns the
     number of caches whose pool grew."""
-    cs = [c for c in caches if isinstance(c, CompressedKV) and c._pending is not None]
+    cs = [c for c in caches if hasattr(c, "finish_page") and c._pending is not None]   # compressed, flat or paged
     if not cs:
         return 0
     cnts = torch.cat([c.cnt for c in cs]).cpu().tolist()

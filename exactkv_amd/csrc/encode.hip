@@ -82,6 +82,12 @@ struct EncArgs {
     int32_t* before;
     int64_t cap;
     int b0, pg0, nb, npg, H, TS;
+    // Paged destination: page pg of source sequence bi goes to page dst_pages[bi *
+    // dst_stride + pg] of the arrays read as B * TS / 16 pages (entries clamped to them);
+    // nullptr: page pg0 + pg of sequence b0 + bi.
+    const int32_t* dst_pages = nullptr;
+    int64_t dst_stride = 0;
+    int64_t all_pages = 0;
 };
 
 __device__ inline void unit_coords(const EncArgs& a, int64_t u, int& bi, int& pg, int& hk) {
@@ -91,8 +97,14 @@ __device__ inline void unit_coords(const EncArgs& a, int64_t u, int& bi, int& pg
     bi = (int)(q / a.npg);
 }
 
+// Page index of unit (bi, pg) in the arrays read as a list of pages.
+__device__ inline int64_t unit_pidx(const EncArgs& a, int bi, int pg) {
+    if (a.dst_pages == nullptr) return (int64_t)(a.b0 + bi) * (a.TS / kPage) + (a.pg0 + pg);
+    const int32_t e = a.dst_pages[bi * a.dst_stride + pg];
+    return (int64_t)min((uint64_t)(uint32_t)e, (uint64_t)(a.all_pages - 1));
+}
 __device__ inline int64_t unit_page(const EncArgs& a, int bi, int pg, int hk) {
-    return ((int64_t)(a.b0 + bi) * (a.TS / kPage) + (a.pg0 + pg)) * a.H + hk;
+    return unit_pidx(a, bi, pg) * a.H + hk;
 }
 
 __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunits) {
@@ -102,7 +114,7 @@ __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunit
     int bi, pg, hk;
     unit_coords(a, u, bi, pg, hk);
     const uint16_t* src = a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h;
-    const int64_t row0 = ((int64_t)(a.b0 + bi) * a.TS + (int64_t)(a.pg0 + pg) * kPage) * a.H + hk;
+    const int64_t row0 = unit_pidx(a, bi, pg) * kPage * a.H + hk;
     const int64_t page = unit_page(a, bi, pg, hk);
     encode_page(src, a.s_p, nullptr, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
                 a.rowmask + page);
@@ -290,6 +302,136 @@ __global__ void bump_kernel(int32_t* state, int TS) {
     if (state[0] < TS) state[0] += 1;
 }
 
+// ---------------------------------------------------------------- paged append
+
+// One token for each of n sequences held in a pool of pages. Sequence slot s (batch row i
+// -> s = slots[i], or i) owns pool pages bt[s * bt_stride + pg] (clamped to the pool) and
+// has lens[s] tokens, the new one included: the caller raises lens before the append, so
+// the new token is token lens[s] - 1 and the kernels never write lens. Its open page is
+// held in the tail area at raw rows cap + (s * H + h) * 16; when the new token fills it,
+// the page is encoded into its pool page and the next table entry is opened.
+struct PagedAppendArgs {
+    const uint16_t* x;        // [n, H, 128] (row strides sx_b, sx_h in elements)
+    int64_t sx_b, sx_h;
+    uint8_t* sm;
+    uint8_t* code;
+    uint8_t* base;
+    int32_t* rowmask;
+    int32_t* rowoff;
+    uint16_t* raw;
+    int32_t* cnt;
+    int32_t* before;
+    const int32_t* slots;     // [n] or nullptr
+    const int32_t* lens;      // [max_seqs]
+    const int32_t* bt;        // [max_seqs, bt_stride]
+    int64_t bt_stride;
+    int64_t cap;
+    int n, H, max_seqs, max_pages, pool_pages;
+};
+
+__device__ inline int paged_slot(const PagedAppendArgs& a, int i) {
+    return a.slots ? min((uint32_t)a.slots[i], (uint32_t)(a.max_seqs - 1)) : i;
+}
+__device__ inline int64_t paged_pidx(const PagedAppendArgs& a, int s, int pg) {
+    return (int64_t)min((uint32_t)a.bt[s * a.bt_stride + pg], (uint32_t)(a.pool_pages - 1));
+}
+// Token index of the new token of slot s, or -1 if it does not fit.
+__device__ inline int paged_new_token(const PagedAppendArgs& a, int s) {
+    const int T = a.lens[s] - 1;
+    return (T >= 0 && T < a.max_pages * kPage) ? T : -1;
+}
+
+__global__ void __launch_bounds__(256) paged_append_write_kernel(PagedAppendArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= a.n * a.H) return;
+    const int i = u / a.H, h = u % a.H;
+    const int s = paged_slot(a, i);
+    const int T = paged_new_token(a, s);
+    if (T < 0) return;
+    const int p = T % kPage;
+    const int64_t tslot = a.cap + ((int64_t)s * a.H + h) * kPage;
+    uint16_t* tail = a.raw + tslot * 128;
+    const uint16_t* x = a.x + i * a.sx_b + h * a.sx_h;
+    tail[p * 128 + lane] = x[lane];
+    tail[p * 128 + lane + 64] = x[lane + 64];
+    if (p != kPage - 1) return;
+    const int pg = T / kPage;
+    const int64_t pidx = paged_pidx(a, s, pg);
+    const int64_t row0 = pidx * kPage * a.H + h;
+    const int64_t page = pidx * a.H + h;
+    encode_page(tail, 128, x, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
+                a.rowmask + page);
+    if (pg + 1 < a.max_pages && lane == 0) {
+        const int64_t next = paged_pidx(a, s, pg + 1) * a.H + h;
+        a.rowmask[next] = 0xFFFF;
+        a.rowoff[next] = (int32_t)tslot;
+    }
+}
+
+// Raw slots for the pages filled by this append, in (batch row, head, token) order.
+__global__ void __launch_bounds__(1024) paged_append_scan_kernel(PagedAppendArgs a) {
+    const int n = a.n * a.H;
+    const int per = (n + 1023) / 1024;
+    const int u0 = threadIdx.x * per, u1 = min(u0 + per, n);
+    const int cnt0 = *a.cnt;
+    int local = 0, filled = 0;
+    for (int u = u0; u < u1; ++u) {
+        const int s = paged_slot(a, u / a.H);
+        const int T = paged_new_token(a, s);
+        if (T < 0 || T % kPage != kPage - 1) continue;
+        filled = 1;
+        local += popc32((uint32_t)a.rowmask[paged_pidx(a, s, T / kPage) * a.H + u % a.H]);
+    }
+    const int any = __syncthreads_or(filled);
+    if (!any) return;                                  // uniform: no page filled, counter untouched
+    int total;
+    int run = cnt0 + block_excl_scan(local, total);
+    for (int u = u0; u < u1; ++u) {
+        const int s = paged_slot(a, u / a.H);
+        const int T = paged_new_token(a, s);
+        if (T < 0 || T % kPage != kPage - 1) continue;
+        const int64_t page = paged_pidx(a, s, T / kPage) * a.H + u % a.H;
+        a.rowoff[page] = run;
+        run += popc32((uint32_t)a.rowmask[page]);
+    }
+    if (threadIdx.x == 0) {
+        *a.before = cnt0;
+        *a.cnt = cnt0 + total;
+    }
+}
+
+__global__ void __launch_bounds__(256) paged_append_rawcopy_kernel(PagedAppendArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= a.n * a.H) return;
+    const int h = u % a.H;
+    const int s = paged_slot(a, u / a.H);
+    const int T = paged_new_token(a, s);
+    if (T < 0 || T % kPage != kPage - 1) return;
+    const int64_t page = paged_pidx(a, s, T / kPage) * a.H + h;
+    const uint32_t m = (uint32_t)a.rowmask[page];
+    if (m == 0) return;
+    copy_raw_rows(a.raw + (a.cap + ((int64_t)s * a.H + h) * kPage) * 128, 128, m, a.rowoff[page], a.cap, a.raw,
+                  lane);
+}
+
+// bf16 twin: pool[(page * 16 + T % 16) * H + h] = x[i, h], page = bt[s, T / 16].
+__global__ void __launch_bounds__(256) paged_bf16_append_kernel(PagedAppendArgs a, uint16_t* buf) {
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= a.n * a.H) return;
+    const int i = u / a.H, h = u % a.H;
+    const int s = paged_slot(a, i);
+    const int T = paged_new_token(a, s);
+    if (T < 0) return;
+    const int64_t row = paged_pidx(a, s, T / kPage) * kPage + T % kPage;
+    uint16_t* d = buf + (row * a.H + h) * 128;
+    const uint16_t* x = a.x + i * a.sx_b + h * a.sx_h;
+    d[lane] = x[lane];
+    d[lane + 64] = x[lane + 64];
+}
+
 // ---------------------------------------------------------------- decode to bf16
 
 struct DecArgs {
@@ -353,6 +495,37 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
     return launch_status("encode_pages");
 }
 
+// Pages of nb source sequences x npg pages into arbitrary pages of B x TS caches read as a
+// list of B * TS / 16 pages: page pg of source sequence bi goes to page dst_pages[bi *
+// dst_stride + pg]. Same kernels, raw-slot order (unit order) and bytes as
+// exkv_encode_pages.
+extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
+                                       void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff,
+                                       void* raw, int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows,
+                                       int32_t B, const int32_t* dst_pages, int64_t dst_stride, int32_t nb,
+                                       int32_t npg, int32_t H, int32_t TS, int32_t D, hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "encode_pages_paged: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages_paged: TS must be a positive multiple of 16 (got %d)", TS);
+    EXKV_REQUIRE(H > 0 && B > 0, "encode_pages_paged: bad H=%d or B=%d", H, B);
+    EXKV_REQUIRE(nb >= 0 && npg >= 0, "encode_pages_paged: negative range");
+    EXKV_REQUIRE(dst_pages && dst_stride >= npg, "encode_pages_paged: need a page table of >= %d columns", npg);
+    EXKV_REQUIRE(cap >= 0 && cap <= raw_rows, "encode_pages_paged: cap %lld exceeds the raw pool (%lld rows)",
+                 (long long)cap, (long long)raw_rows);
+    EXKV_REQUIRE(src && sm && code && base && rowmask && rowoff && raw && cnt, "encode_pages_paged: null pointer");
+    const int64_t n = (int64_t)nb * npg * H;
+    if (n == 0) return EXKV_OK;
+    EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
+              rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, 0, 0, nb, npg, H, TS};
+    a.dst_pages = dst_pages;
+    a.dst_stride = dst_stride;
+    a.all_pages = (int64_t)B * (TS / kPage);
+    const unsigned grid = (unsigned)((n + 3) / 4);
+    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, a, n);
+    hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    return launch_status("encode_pages_paged");
+}
+
 extern "C" int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
                                  int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
                                  int32_t* state, int64_t cap, int64_t raw_rows, int32_t B, int32_t H,
@@ -381,6 +554,56 @@ extern "C" int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void*
                        (const uint16_t*)x, sx_b, sx_h, (uint16_t*)buf, (const int32_t*)state, B, H, TS);
     hipLaunchKernelGGL(bump_kernel, dim3(1), dim3(1), 0, stream, state, TS);
     return launch_status("bf16_append");
+}
+
+static int check_paged_append(const char* what, int32_t n, int32_t H, int32_t D, int32_t max_seqs,
+                              int32_t max_pages, int64_t bt_stride, int32_t pool_pages) {
+    EXKV_REQUIRE(D == kD, "%s: head dim must be 128 (got %d)", what, D);
+    EXKV_REQUIRE(n >= 0 && H > 0 && max_seqs > 0 && n <= max_seqs, "%s: bad shape n=%d H=%d max_seqs=%d", what, n,
+                 H, max_seqs);
+    EXKV_REQUIRE(max_pages > 0 && bt_stride >= max_pages && pool_pages > 0,
+                 "%s: bad page table (max_pages=%d stride=%lld pool=%d)", what, max_pages, (long long)bt_stride,
+                 pool_pages);
+    return EXKV_OK;
+}
+
+extern "C" int exkv_cache_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
+                                       int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
+                                       int64_t cap, int64_t raw_rows, const int32_t* slots, const int32_t* lens,
+                                       const int32_t* block_table, int64_t bt_stride, int32_t n, int32_t H,
+                                       int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
+                                       hipStream_t stream) {
+    const int rc = check_paged_append("append_paged", n, H, D, max_seqs, max_pages, bt_stride, pool_pages);
+    if (rc != EXKV_OK) return rc;
+    EXKV_REQUIRE(cap >= 0 && cap + (int64_t)max_seqs * H * kPage <= raw_rows,
+                 "append_paged: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
+    EXKV_REQUIRE(x && sm && code && base && rowmask && rowoff && raw && cnt && before && lens && block_table,
+                 "append_paged: null pointer");
+    if (n == 0) return EXKV_OK;
+    PagedAppendArgs a{(const uint16_t*)x, sx_b, sx_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base, rowmask,
+                      rowoff, (uint16_t*)raw, cnt, before, slots, lens, block_table, bt_stride, cap, n, H,
+                      max_seqs, max_pages, pool_pages};
+    const unsigned grid = (unsigned)((n * H + 3) / 4);
+    hipLaunchKernelGGL(paged_append_write_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(paged_append_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(paged_append_rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a);
+    return launch_status("cache_append_paged");
+}
+
+extern "C" int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf, const int32_t* slots,
+                                      const int32_t* lens, const int32_t* block_table, int64_t bt_stride, int32_t n,
+                                      int32_t H, int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
+                                      hipStream_t stream) {
+    const int rc = check_paged_append("bf16_append_paged", n, H, D, max_seqs, max_pages, bt_stride, pool_pages);
+    if (rc != EXKV_OK) return rc;
+    EXKV_REQUIRE(x && buf && lens && block_table, "bf16_append_paged: null pointer");
+    if (n == 0) return EXKV_OK;
+    PagedAppendArgs a{(const uint16_t*)x, sx_b, sx_h, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, slots, lens, block_table, bt_stride, 0, n, H, max_seqs, max_pages,
+                      pool_pages};
+    hipLaunchKernelGGL(paged_bf16_append_kernel, dim3((unsigned)((n * H + 3) / 4)), dim3(256), 0, stream, a,
+                       (uint16_t*)buf);
+    return launch_status("bf16_append_paged");
 }
 
 extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,

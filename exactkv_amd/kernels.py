@@ -245,3 +245,52 @@ def encode_pages(src, strides, buf, b0, pg0, nb, npg):
               _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4),
               _lib.ptr(before, align=4) if before is not None else None, int(buf["cap"]), raw.shape[0],
               buf["sm"].shape[0], int(b0), int(pg0), int(nb), int(npg), H, TS, D, _lib.stream())
+
+
+def encode_pages_paged(src, strides, buf, dst_pages, nb, npg):
+    """encode_pages into a paged cache: page pg of source sequence bi (strides as in
+    encode_pages) goes to page dst_pages[bi, pg] of the cache's arrays read as a list of
+    B * TS / 16 pages. dst_pages: int32 [>= nb, >= npg] on the GPU."""
+    H, TS, D = buf["H"], buf["TS"], buf["D"]
+    _check_source(src, strides, nb, npg, H)
+    if (dst_pages.dtype != torch.int32 or dst_pages.dim() != 2 or dst_pages.stride(1) != 1 or dst_pages.shape[0] < nb
+            or dst_pages.shape[1] < npg):
+        raise ValueError("dst_pages must be an int32 [nb, npg] tensor with unit column stride")
+    raw = buf["raw"]
+    before = buf.get("before")
+    _lib.call("exkv_encode_pages_paged", _lib.ptr(src, align=2, what="src"), *[int(s) for s in strides],
+              _lib.ptr(buf["sm"]), _lib.ptr(buf["code"]), _lib.ptr(buf["base"]), _lib.ptr(buf["rowmask"]),
+              _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4),
+              _lib.ptr(before, align=4) if before is not None else None, int(buf["cap"]), raw.shape[0],
+              buf["sm"].shape[0], _lib.ptr(dst_pages, align=4, what="dst_pages"), dst_pages.stride(0), int(nb), int(npg), H,
+              TS, D, _lib.stream())
+
+
+def _paged_append_args(x, table, slots):
+    n, H, D = x.shape
+    if x.dtype != torch.bfloat16 or x.stride(2) != 1:
+        raise ValueError(f"append expects a bf16 [n, H, {D}] tensor with contiguous rows")
+    bt, lens = table.block_table, table.lens
+    if slots is not None and (slots.dtype != torch.int32 or slots.numel() != n or not slots.is_contiguous()):
+        raise ValueError("slots must be a contiguous int32 tensor with one entry per row of x")
+    return ((_lib.ptr(slots, align=4, what="slots") if slots is not None else None), _lib.ptr(lens, align=4),
+            _lib.ptr(bt, what="block_table"), bt.stride(0), n, H, bt.shape[0], bt.shape[1])
+
+
+def append_paged(x, buf, table, slots=None):
+    """One token per row of x [n, H, 128] into a paged compressed cache (buf as for
+    encode_pages, arrays of a [1, 16 * pool_pages, H, 128] cache) whose slots, lengths and
+    block table are those of `table` (lens already counting the new token)."""
+    sp, lp, bp, bts, n, H, ms, mp = _paged_append_args(x, table, slots)
+    raw = buf["raw"]
+    _lib.call("exkv_cache_append_paged", _lib.ptr(x, align=2, what="x"), x.stride(0), x.stride(1),
+              _lib.ptr(buf["sm"]), _lib.ptr(buf["code"]), _lib.ptr(buf["base"]), _lib.ptr(buf["rowmask"]),
+              _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4), _lib.ptr(buf["before"], align=4),
+              int(buf["cap"]), raw.shape[0], sp, lp, bp, bts, n, H, ms, mp, buf["TS"] // P, buf["D"], _lib.stream())
+
+
+def append_paged_bf16(x, pool, table, slots=None):
+    """bf16 twin of append_paged over pool [1, 16 * pool_pages, H, 128]."""
+    sp, lp, bp, bts, n, H, ms, mp = _paged_append_args(x, table, slots)
+    _lib.call("exkv_bf16_append_paged", _lib.ptr(x, align=2, what="x"), x.stride(0), x.stride(1), _lib.ptr(pool),
+              sp, lp, bp, bts, n, H, ms, mp, pool.shape[0] * pool.shape[1] // P, x.shape[2], _lib.stream())

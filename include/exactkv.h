@@ -50,6 +50,17 @@ int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, i
                       int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
                       int32_t D, hipStream_t stream);
 
+/* The page encoder into a paged cache: page pg of source sequence bi goes to page
+ * dst_pages[bi*dst_stride + pg] of the B x TS arrays read as a list of B*TS/16 pages (entries
+ * clamped to it). Same bytes and raw-slot order as exkv_encode_pages.
+ * No counterpart in the reference (contiguous caches only); paged KV is in its future
+ * work (README.md:121-123). */
+int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
+                            void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
+                            int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
+                            const int32_t* dst_pages, int64_t dst_stride, int32_t nb, int32_t npg, int32_t H,
+                            int32_t TS, int32_t D, hipStream_t stream);
+
 /* Append one token per sequence (x: [B, H, 128] bf16, row strides sx_b, sx_h) to the cache
  * whose token count is state[0] (device): write it into the tail area; when it completes
  * page T/16, encode that page (slots as above, *before = counter before) and open the next
@@ -65,6 +76,33 @@ int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void*
  * Replaces: cache.py:141-143 BF16KV.append. */
 int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void* buf, int32_t* state, int32_t B,
                      int32_t H, int32_t TS, int32_t D, hipStream_t stream);
+
+/* Append one token for each of n sequences of a paged cache: a pool of pool_pages pages
+ * (arrays as a [1, 16 * pool_pages, H, 128] cache) shared by max_seqs sequence slots.
+ * Batch row i is slot slots[i] (slots == NULL: slot i; the slots must differ); slot s owns
+ * pool pages block_table[s * bt_stride + pg] (pg < max_pages, entries clamped to the
+ * pool) and holds lens[s] tokens, the new one included (the caller raises lens first; the
+ * call never writes it). Slot s's open page is held in the tail area at raw rows
+ * cap + (s * H + h) * 16 (raw_rows >= cap + max_seqs * H * 16). When the new token
+ * fills page pg, that page is encoded into its pool page (raw slots in (row, head, token)
+ * order from *cnt, *before = counter before) and table entry pg + 1, which the caller
+ * has filled, is opened (rowmask 0xFFFF, rowoff into the tail area).
+ * No counterpart in the reference (contiguous caches only); paged KV is in its future
+ * work (README.md:121-123). The per-sequence steps are those of cache.py:100-112. */
+int exkv_cache_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
+                            int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
+                            int64_t cap, int64_t raw_rows, const int32_t* slots, const int32_t* lens,
+                            const int32_t* block_table, int64_t bt_stride, int32_t n, int32_t H,
+                            int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
+                            hipStream_t stream);
+
+/* bf16 twin of exkv_cache_append_paged over a pool buf [16 * pool_pages, H, 128]: token
+ * lens[s] - 1 of slot s goes to row (block_table[s, t / 16] * 16 + t % 16).
+ * No counterpart in the reference (see exkv_cache_append_paged). */
+int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf, const int32_t* slots,
+                           const int32_t* lens, const int32_t* block_table, int64_t bt_stride, int32_t n,
+                           int32_t H, int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
+                           hipStream_t stream);
 
 /* Compressed cache -> bf16 out [B, T, H, 128] through the attention kernels' page decoder.
  * Replaces: kernels.py:331-337 decode_to_bf16 (_dec_only_kernel :197-211). */

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+import exactkv_amd as exactkv
 from exactkv_amd import kernels, synthetic
 from oracle import attention as oatt
 from tests.conftest import same_bits, u16
@@ -99,3 +100,143 @@ def test_paged_bad_arguments_raise():
         kernels.attention_reference(q, k, k, 16, block_table=torch.zeros(1, 2, dtype=torch.int64, device=DEV))
     with pytest.raises(RuntimeError, match="exceeds|outside"):
         kernels.attention_reference(q, k, k, 48, block_table=torch.zeros(1, 2, dtype=torch.int32, device=DEV))
+
+
+def test_paged_encoder_bytes_match_contiguous():
+    """encode_pages_paged writes, at each mapped pool page, the bytes encode_pages writes
+    at the contiguous page (same raw-slot order, so rowoff and raw agree too)."""
+    B, TS, H = 3, 512, 8
+    npg = TS // P
+    x = synthetic.make_kv(B, TS, H, kind="k", seed=71, raw_row_rate=0.02).to(DEV)
+    pool_pages = B * npg + 9
+    table = torch.randperm(pool_pages, generator=torch.Generator().manual_seed(8))[:B * npg].view(B, npg)
+    c = _encode(x)
+    pool = exactkv.CompressedKV(1, pool_pages * P, H, 128, reserve=1.0)
+    st = (x.stride(0), P * x.stride(1), x.stride(1), x.stride(2))
+    _say("paged encode", B, TS, H, pool_pages)
+    kernels.encode_pages_paged(x, st, pool._buf(), table.to(torch.int32).to(DEV), B, npg)
+    n = int(c.cnt.item())
+    assert n > 0 and int(pool.cnt.item()) == n
+    tl = table.reshape(-1).to(DEV)
+    rows = (tl[:, None] * P + torch.arange(P, device=DEV)[None, :]).reshape(-1)
+    assert torch.equal(pool.sm[0][rows], c.sm.reshape(-1, H, 128))
+    assert torch.equal(pool.code[0][rows], c.code.reshape(-1, H, 64))
+    assert torch.equal(pool.base[0][tl], c.base.reshape(-1, H, 128))
+    assert torch.equal(pool.rowmask[0][tl], c.rowmask.reshape(-1, H))
+    assert torch.equal(pool.rowoff[0][tl], c.rowoff.reshape(-1, H))
+    assert torch.equal(pool.raw[:n], c.raw[:n])
+
+
+def _gather(pool_bf16, pages, T):
+    rows = (torch.tensor(pages)[:, None] * P + torch.arange(P)[None, :]).reshape(-1)[:T]
+    return pool_bf16[0][rows.to(pool_bf16.device)]
+
+
+def test_paged_cache_prefill_append_release_compact():
+    """A PageTable shared by paged K/V caches and their bf16 twins: prefills of ragged
+    lengths, decode steps over dense and permuted slot subsets, a forced raw-pool overflow,
+    release + reuse of pages and compact(). After every step the compressed and bf16 paged
+    attention agree bit for bit; the decoded pool equals the tokens written."""
+    H, Hq, D = 4, 16, 128
+    table = exactkv.PageTable(num_pages=64, max_seqs=4, max_pages=16)
+    kc, vc = exactkv.PagedCompressedKV(table, H, reserve=1e-4), exactkv.PagedCompressedKV(table, H, reserve=1e-4)
+    kb, vb = exactkv.PagedBF16KV(table, H), exactkv.PagedBF16KV(table, H)
+    src_k = synthetic.make_kv(6, 256, H, kind="k", seed=81, raw_row_rate=0.05)
+    src_v = synthetic.make_kv(6, 256, H, kind="v", seed=82, raw_row_rate=0.05)
+    truth = {}                                          # slot -> (k rows, v rows) on the CPU
+
+    def prefill(seq, T):
+        s = table.add(T)
+        k, v = src_k[seq:seq + 1, :T], src_v[seq:seq + 1, :T]
+        for c, x in ((kc, k), (vc, v), (kb, k), (vb, v)):
+            c.prefill(s, x.to(DEV).contiguous())
+        truth[s] = [list(k[0]), list(v[0]), seq]
+        return s
+
+    def step(slots, check=True):
+        table.begin_step(slots)
+        rows = table._step_slots
+        xk = torch.stack([src_k[truth[s][2], len(truth[s][0])] for s in rows])
+        xv = torch.stack([src_v[truth[s][2], len(truth[s][1])] for s in rows])
+        for s, a, b in zip(rows, xk, xv):
+            truth[s][0].append(a)
+            truth[s][1].append(b)
+        for c, x in ((kc, xk), (vc, xv), (kb, xk), (vb, xv)):
+            c.append(x.to(DEV).contiguous())
+        if check:
+            q = synthetic.make_q(len(rows), Hq, seed=table.step).to(DEV)
+            o_c = exactkv.decode_attention(q, kc, vc)
+            o_b = exactkv.decode_attention(q, kb, vb)
+            assert same_bits(o_c, o_b), f"step {table.step}"
+        exactkv.check_overflow([kc, vc])
+
+    def check_contents():
+        for c, b in ((kc, kb), (vc, vb)):
+            dec = kernels.decode_to_bf16(c.buffers(), c.TS)
+            for s in table.live_slots():
+                pages, T = table.pages(s), table.length(s)
+                want = torch.stack(truth[s][0 if c is kc else 1]).to(DEV) if T else None
+                if T:
+                    assert same_bits(_gather(dec, pages, T), want), f"slot {s}"
+                    assert same_bits(_gather(b.buf, pages, T), want)
+
+    _say("paged cache: prefill 37, 16, 100, 0")
+    for seq, T in enumerate((37, 16, 100, 0)):
+        prefill(seq, T)
+    check_contents()
+    for i in range(20):
+        step(None)
+    _say("paged cache: permuted subsets")
+    for i in range(12):
+        step([3, 1] if i % 2 else [2, 0, 3])
+    check_contents()
+    _say("paged cache: forced overflow")
+    grows = kc.grows
+    kc.cnt.fill_(kc.cap + 1)                            # the next filled pages overflow the pool
+    for i in range(40):                                 # attention would read dropped rows until repaired
+        step(None, check=False)
+        if kc.grows > grows:
+            break
+    assert kc.grows > grows and int(kc.cnt.item()) >= int(kc._before.item()) > 0
+    check_contents()
+    step(None)
+    _say("paged cache: release, reuse, compact")
+    table.release(1)
+    del truth[1]
+    assert prefill(4, 61) == 1                          # the lowest free slot, reusing freed pages
+    for i in range(18):
+        step(None)
+    assert kc.compact() > 0                             # the overflow left a gap; slot 1's old rows
+    vc.compact()
+    check_contents()
+    step(None)
+    check_contents()
+    rows = table._step_slots
+    lens = [table.length(s) for s in rows]
+    Tm = max(lens)
+    kk = torch.zeros(len(rows), Tm, H, D, dtype=torch.bfloat16)
+    vv = torch.zeros_like(kk)
+    for i, s in enumerate(rows):
+        kk[i, :lens[i]] = torch.stack(truth[s][0])
+        vv[i, :lens[i]] = torch.stack(truth[s][1])
+    q = synthetic.make_q(len(rows), Hq, seed=table.step)
+    _say("paged cache: oracle", lens)
+    o_c = exactkv.decode_attention(q.to(DEV), kc, vc)
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(kk), u16(vv), Tm, np.float32, lens=lens))
+
+
+def test_paged_table_errors():
+    table = exactkv.PageTable(num_pages=4, max_seqs=2, max_pages=4)
+    kc = exactkv.PagedCompressedKV(table, 2)
+    with pytest.raises(ValueError):
+        table.add(65)                                   # beyond 4 pages of 16
+    s = table.add(30)
+    with pytest.raises(RuntimeError, match="begin_step"):
+        kc.append(torch.zeros(1, 2, 128, dtype=torch.bfloat16, device=DEV))
+    table.begin_step([s])
+    with pytest.raises(ValueError):
+        kc.append(torch.zeros(2, 2, 128, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):
+        table.begin_step([s, s])
+    with pytest.raises(RuntimeError, match="exhausted"):
+        table.add(40)                                   # 3 pages, 2 free

@@ -42,6 +42,15 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
     with pytest.raises(RuntimeError, match="split_len"):
         _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0.1, None)
+    # paged entry points: a page table narrower than the pages to encode, a raw pool
+    # without room for the tail areas, more rows than sequence slots
+    rc = lib.exkv_encode_pages_paged(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 1, 1, 2, 1, 3, 4, 64, 128, None)
+    assert rc == 1 and b"page table" in lib.exkv_last_error()
+    rc = lib.exkv_cache_append_paged(1, 0, 0, 1, 1, 1, 1, 1, 1, 1, 1, 10, 100, None, 1, 1, 8, 2, 4, 2, 8, 16, 128,
+                                     None)
+    assert rc == 1 and b"tail area" in lib.exkv_last_error()
+    rc = lib.exkv_bf16_append_paged(1, 0, 0, 1, None, 1, 1, 8, 3, 4, 2, 8, 16, 128, None)
+    assert rc == 1 and b"bad shape" in lib.exkv_last_error()
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,expect", [

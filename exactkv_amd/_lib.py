@@ -42,6 +42,10 @@ SIGNATURES = {
                                          _i32, _f32, _p],
     "exkv_attn_bf16_paged": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                              _p, _i64, _i32, _i32, _f32, _p],
+    "exkv_wire_bytes": [_i32, _i32, _i64],
+    "exkv_wire_pack": [_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _i64, _p],
+    "exkv_wire_unpack": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32,
+                         _p, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],
@@ -68,7 +72,7 @@ def load():
     for name, args in SIGNATURES.items():
         f = getattr(lib, name)
         f.argtypes = args
-        f.restype = ctypes.c_char_p if name == "exkv_last_error" else ctypes.c_int
+        f.restype = {"exkv_last_error": ctypes.c_char_p, "exkv_wire_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
     v = lib.exkv_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libexactkv_hip.so ABI version {v}, expected {ABI_VERSION}: rebuild the library")

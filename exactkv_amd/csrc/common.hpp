@@ -71,6 +71,29 @@ __host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t bm, u
 
 __device__ inline int popc32(uint32_t x) { return __builtin_popcount(x); }
 
+// Block-wide exclusive scan of one int per thread (1024 threads).
+__device__ inline int block_excl_scan(int v, int& total) {
+    __shared__ int wsum[16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    int wpre = 0;
+    total = 0;
+    for (int i = 0; i < 16; ++i) {
+        const int s = wsum[i];
+        if (i < w) wpre += s;
+        total += s;
+    }
+    __syncthreads();
+    return wpre + inc - v;
+}
+
 }  // namespace exkv
 
 // ---------------------------------------------------------------- C-ABI error plumbing

@@ -120,29 +120,6 @@ __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunit
                 a.rowmask + page);
 }
 
-// Block-wide exclusive scan of one int per thread (1024 threads).
-__device__ inline int block_excl_scan(int v, int& total) {
-    __shared__ int wsum[16];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(inc, off);
-        if (lane >= off) inc += y;
-    }
-    if (lane == 63) wsum[w] = inc;
-    __syncthreads();
-    int wpre = 0;
-    total = 0;
-    for (int i = 0; i < 16; ++i) {
-        const int s = wsum[i];
-        if (i < w) wpre += s;
-        total += s;
-    }
-    __syncthreads();
-    return wpre + inc - v;
-}
-
 __global__ void __launch_bounds__(1024) scan_kernel(EncArgs a, int64_t nunits) {
     const int64_t per = (nunits + 1023) / 1024;
     const int64_t u0 = threadIdx.x * per;

@@ -166,7 +166,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged"])
+    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -181,11 +181,11 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload in ("e2e", "c3", "c2a_paged"):
+    if a.workload in ("e2e", "c3", "c2a_paged", "wire"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
-        return e2e(a) if a.workload == "e2e" else c3_stress(a) if a.workload == "c3" else paged_c2a(a)
+        return {"e2e": e2e, "c3": c3_stress, "c2a_paged": paged_c2a, "wire": wire_bench}[a.workload](a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -337,6 +337,101 @@ def paged_c2a(a):
                      "kernel_us": round(ms_split * 1e3, 2)},
         "bf16_twin_us": round(ms_b * 1e3, 2), "speedup_vs_bf16": round(ms_b / ms_c, 3),
         "bit_identical_to_bf16": bool(identical), "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(res), flush=True)
+
+
+def wire_bench(a):
+    """Wire form at c2a's shape: pack the 8 sequences of a K and a V cache (B8 x 8192, 8 KV
+    heads) into preallocated blobs (one pack call per cache per step), and unpack them into a
+    second pair of caches (one unpack call per cache per step). HIP events around the
+    launches; cache copies rotated. Algorithmic bytes per step: every blob byte read once and written once."""
+    import numpy as np
+    import torch
+    import exactkv_amd as exactkv
+    from exactkv_amd import _lib, kernels, synthetic, wire
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, T, H = 8, 8192, 8
+    print("[wire] generating data", file=sys.stderr, flush=True)
+    copies, raw_src = [], None
+    for i in range(a.copies):
+        pair = []
+        for kind, seed in (("k", 600 + i), ("v", 700 + i)):
+            x = synthetic.make_kv(B, T, H, kind=kind, seed=seed, device=dev)
+            c = exactkv.CompressedKV(B, T, H, 128)
+            for b in range(B):
+                c.prefill_slot(b, x[b:b + 1])
+            pair.append(c)
+            if i == 0 and kind == "k":
+                raw_src = x
+        copies.append(pair)
+    blobs = [[wire.pack(c, b) for b in range(B)] for c in copies[0]]
+    sizes = [[int(bl.numel()) for bl in row] for row in blobs]
+    total = sum(map(sum, sizes))
+    dst = [exactkv.CompressedKV(B, T, H, 128, reserve=0.02) for _ in range(2)]
+    for c, row in zip(dst, blobs):
+        for b in range(B):
+            wire.unpack(row[b], c, b)
+    identical = all(torch.equal(kernels.decode_to_bf16(d.buffers(), T).view(torch.int16),
+                                kernels.decode_to_bf16(s.buffers(), T).view(torch.int16))
+                    for d, s in zip(dst, copies[0]))
+    # one pack call per cache (8 sequences, two launches); one unpack call per cache
+    pargs = [[wire._batch_args(c, list(range(B)), [wire._sequence(c, b) for b in range(B)], row, dev)
+              for c, row in zip(pair, blobs)] for pair in copies]
+    st = _lib.stream()
+
+    def pack_all(i):
+        for c, (d, width, max_t, wss) in zip(copies[i], pargs[i]):
+            _lib.call("exkv_wire_pack", c.sm.data_ptr(), c.code.data_ptr(), c.base.data_ptr(), c.rowmask.data_ptr(),
+                      c.rowoff.data_ptr(), c.raw.data_ptr(), c.raw.shape[0], B * (T // 16), B, d["pages"].data_ptr(),
+                      width, d["tokens"].data_ptr(), d["tails"].data_ptr(), d["blobs"].data_ptr(),
+                      d["sizes"].data_ptr(), max_t, H, 128, d["ws"].data_ptr(), wss, st)
+
+    dargs = [wire._batch_args(c, list(range(B)), [wire._sequence(c, b) for b in range(B)], row, dev)
+             for c, row in zip(dst, blobs)]
+
+    def unpack_all(i):
+        for c, (d, width, max_t, wss) in zip(dst, dargs):
+            c.cnt.zero_()
+            _lib.call("exkv_wire_unpack", c.sm.data_ptr(), c.code.data_ptr(), c.base.data_ptr(), c.rowmask.data_ptr(),
+                      c.rowoff.data_ptr(), c.raw.data_ptr(), c.raw.shape[0], c.cap, c.cnt.data_ptr(),
+                      c._before.data_ptr(), B * (T // 16), B, d["pages"].data_ptr(), width, d["tokens"].data_ptr(),
+                      d["open"].data_ptr(), d["tails"].data_ptr(), d["blobs"].data_ptr(), d["sizes"].data_ptr(),
+                      max_t, H, 128, d["ws"].data_ptr(), wss, st)
+
+    ms_pack = time_loop(pack_all, a.steps, a.warmup, a.copies)
+    ms_unpack = time_loop(unpack_all, a.steps, a.warmup, 1)
+    gb_pack = 2 * total / (ms_pack * 1e-3) / 1e9
+    gb_unpack = 2 * total / (ms_unpack * 1e-3) / 1e9
+    bf16_bytes = 2 * B * T * H * 128 * 2
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import wire as owire
+        x0 = raw_src[0].cpu().view(torch.int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        n = 0
+        while True:                                    # one sequence's K at a time, >= cpu-seconds / 4
+            owire.pack(x0)
+            n += 1
+            if time.perf_counter() - t0 >= a.cpu_seconds / 4:
+                break
+        per_seq = (time.perf_counter() - t0) / n
+        cpu = {"value": round(2 * sizes[0][0] / per_seq / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"oracle wire.pack (numpy encode + layout) of one 8192 x 8-head key sequence, {n} passes"}
+    res = {
+        "metric": "wire pack GB/s (blob bytes read + written) at c2a shape", "value": round(gb_pack, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_pack, 5),
+        "higher_is_better": True, "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "wire: pack / unpack 8 sequences x (K, V) of B8 x 8192 x 8 heads", "B": B, "T": T,
+                   "H": H, "blob_bytes": total, "bf16_bytes": bf16_bytes, "cache_copies": a.copies},
+        "roofline": {"bound": "hbm", "achieved": round(gb_pack, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gb_pack / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "wire_scan_kernel + wire_copy_kernel (2 calls x 8 sequences)", "algorithmic_bytes": 2 * total},
+        "unpack_GBps": round(gb_unpack, 1), "unpack_ms": round(ms_unpack, 5),
+        "blob_vs_bf16": round(total / bf16_bytes, 4), "roundtrip_identical": bool(identical),
+        "cpu_baseline": cpu, "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(res), flush=True)
 

@@ -43,9 +43,10 @@ SIGNATURES = {
     "exkv_attn_bf16_paged": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                              _p, _i64, _i32, _i32, _f32, _p],
     "exkv_wire_bytes": [_i32, _i32, _i64],
-    "exkv_wire_pack": [_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _i64, _p],
-    "exkv_wire_unpack": [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _i32, _i64, _i64, _i32, _i32, _i32,
-                         _p, _p],
+    "exkv_wire_pack": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i32, _i32, _i32, _p,
+                       _i64, _p],
+    "exkv_wire_unpack": [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _i32,
+                         _i32, _i32, _p, _i64, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],

@@ -1,4 +1,4 @@
-"""Wire form of one sequence's compressed cache: pack it into one contiguous byte blob
+"""Wire form of a sequence's compressed cache: pack it into one contiguous byte blob
 (KV offload to host memory or disk, transfer between pools, processes or GPUs) and
 unpack it into a contiguous or paged cache, on the GPU.
 
@@ -58,7 +58,7 @@ def _sequence(cache, seq):
     H = cache.H
     if isinstance(cache, PagedCompressedKV):
         t = cache.table
-        if t._pages[seq] is None:
+        if not 0 <= seq < t.max_seqs or t._pages[seq] is None:
             raise ValueError(f"slot {seq} is not in use")
         T = t.length(seq)
         return T, list(t._pages[seq]), cache.cap + seq * H * P, t.num_pages, T // P < t.max_pages
@@ -71,35 +71,60 @@ def _sequence(cache, seq):
     raise TypeError(type(cache))
 
 
-def _pages_arg(pages, n, dev):
-    return torch.tensor(pages[:max(n, 1)], dtype=torch.int32).to(dev)
+def _batch_args(cache, seqs, infos, blobs, dev):
+    """Device arrays of one pack / unpack call."""
+    width = max(max(len(i[1]) for i in infos), 1)
+    pages = torch.zeros(len(seqs), width, dtype=torch.int32)
+    for r, i in enumerate(infos):
+        pages[r, :len(i[1])] = torch.tensor(i[1], dtype=torch.int32)
+    max_t = max(i[0] for i in infos)
+    ws_stride = (max_t // P) * cache.H + 3
+    host = dict(pages=pages, tokens=torch.tensor([i[0] for i in infos], dtype=torch.int32),
+                tails=torch.tensor([i[2] for i in infos], dtype=torch.int64),
+                blobs=torch.tensor([_lib.ptr(b, align=256, what="blob") for b in blobs], dtype=torch.int64),
+                sizes=torch.tensor([b.numel() for b in blobs], dtype=torch.int64),
+                open=torch.tensor([int(i[4]) for i in infos], dtype=torch.int32))
+    d = {k: v.to(dev) for k, v in host.items()}
+    d["ws"] = torch.empty(len(seqs), ws_stride, dtype=torch.int32, device=dev)
+    return d, width, max_t, ws_stride
 
 
 def pack(cache, seq):
     """Sequence `seq` (a CompressedKV slot b, or a PagedCompressedKV slot) -> uint8 blob on
     the cache's GPU. Synchronises once (to size the blob)."""
+    return pack_many(cache, [seq])[0]
+
+
+def pack_many(cache, seqs):
+    """Blobs of several sequences of one cache, packed by one call (two launches)."""
     if cache._pending is not None:
         raise RuntimeError("call check_overflow() before packing")
-    T, pages, tail_row, pool_pages, _ = _sequence(cache, seq)
-    H, npf = cache.H, T // P
-    dev = cache.sm.device
-    pg = _pages_arg(pages, npf, dev)
-    N = int(_popc16(cache.rowmask.view(-1, H).index_select(0, pg[:npf].long()) & 0xFFFF).sum().item()) if npf else 0
-    size = nbytes(H, T, N)
-    blob = torch.empty(size, dtype=torch.uint8, device=dev)
-    ws = torch.empty(npf * H + 2, dtype=torch.int32, device=dev)
-    raw = cache.raw
+    seqs = list(seqs)
+    if not seqs:
+        return []
+    H, dev = cache.H, cache.sm.device
+    infos = [_sequence(cache, s) for s in seqs]
+    full = [p for i in infos for p in i[1][:i[0] // P]]
+    counts = [0] * len(seqs)
+    if full:
+        rm = cache.rowmask.view(-1, H).index_select(0, torch.tensor(full, dtype=torch.int64, device=dev))
+        per_page = _popc16(rm & 0xFFFF).sum(1).cpu().tolist()
+        k = 0
+        for r, i in enumerate(infos):
+            n = i[0] // P
+            counts[r] = int(sum(per_page[k:k + n]))
+            k += n
+    blobs = [torch.empty(nbytes(H, i[0], n), dtype=torch.uint8, device=dev) for i, n in zip(infos, counts)]
+    d, width, max_t, ws_stride = _batch_args(cache, seqs, infos, blobs, dev)
     _lib.call("exkv_wire_pack", _lib.ptr(cache.sm), _lib.ptr(cache.code), _lib.ptr(cache.base),
-              _lib.ptr(cache.rowmask), _lib.ptr(cache.rowoff), _lib.ptr(raw), raw.shape[0], _lib.ptr(pg, align=4),
-              pool_pages, tail_row, H, T, cache.D, _lib.ptr(ws, align=4), _lib.ptr(blob, align=256, what="blob"),
-              size, _lib.stream())
-    return blob
+              _lib.ptr(cache.rowmask), _lib.ptr(cache.rowoff), _lib.ptr(cache.raw), cache.raw.shape[0], infos[0][3],
+              len(seqs), d["pages"].data_ptr(), width, d["tokens"].data_ptr(), d["tails"].data_ptr(),
+              d["blobs"].data_ptr(), d["sizes"].data_ptr(), max_t, H, cache.D, d["ws"].data_ptr(), ws_stride,
+              _lib.stream())
+    return blobs
 
 
-def unpack(blob, cache, seq):
-    """Write a blob into sequence `seq` of `cache`: a CompressedKV slot b (the cache then
-    holds the blob's T tokens, as after prefill_slot) or a PagedCompressedKV slot already
-    added with table.add(T) for the blob's T. The raw pool grows first if needed."""
+def _check_blob(blob, cache):
     h = header(blob)
     if h["magic"] != MAGIC or h["version"] != VERSION:
         raise ValueError(f"not an exactkv wire blob (magic {h['magic']:#x}, version {h['version']})")
@@ -110,29 +135,48 @@ def unpack(blob, cache, seq):
         raise ValueError("inconsistent wire header")
     if blob.numel() < h["total"]:
         raise ValueError(f"blob of {blob.numel()} bytes is shorter than its header's {h['total']}")
-    if not blob.is_cuda or blob.device != cache.sm.device:
-        blob = blob.to(cache.sm.device)
+    return h
+
+
+def unpack(blob, cache, seq):
+    """Write a blob into sequence `seq` of `cache`: a CompressedKV slot b (the cache then
+    holds the blob's T tokens, as after prefill_slot) or a PagedCompressedKV slot already
+    added with table.add(T) for the blob's T. The raw pool grows first if needed."""
+    unpack_many([blob], cache, [seq])
+
+
+def unpack_many(blobs, cache, seqs):
+    """unpack for several blobs and sequences of one cache in one call (two launches)."""
+    seqs = list(seqs)
+    if len(blobs) != len(seqs) or len(set(seqs)) != len(seqs):
+        raise ValueError("one distinct sequence per blob")
+    if not seqs:
+        return
+    heads = [_check_blob(b, cache) for b in blobs]
+    dev = cache.sm.device
+    blobs = [b if b.device == dev else b.to(dev) for b in blobs]
     if cache._pending is not None:
         raise RuntimeError("call check_overflow() before unpacking")
+    Ts = [h["tokens"] for h in heads]
     if isinstance(cache, CompressedKV):
-        if T > cache.TS:
-            raise ValueError(f"blob of {T} tokens into a cache of {cache.TS}")
-        cache.T = T
-        cache.state[0] = T
-    elif isinstance(cache, PagedCompressedKV) and cache.table.length(seq) != T:
-        raise ValueError(f"blob of {T} tokens into a slot of {cache.table.length(seq)}")
-    _, pages, _, pool_pages, open_page = _sequence(cache, seq)
+        if len(set(Ts)) != 1 or Ts[0] > cache.TS:
+            raise ValueError(f"blobs of {sorted(set(Ts))} tokens into a cache of {cache.TS} (one length per cache)")
+        cache.T = Ts[0]
+        cache.state[0] = Ts[0]
+    else:
+        for s, T in zip(seqs, Ts):
+            if cache.table.length(s) != T:
+                raise ValueError(f"blob of {T} tokens into a slot of {cache.table.length(s)}")
+    N = sum(h["raw_rows"] for h in heads)
     cnt = int(cache.cnt.item())
     if cnt + N > cache.cap:
         cache._grow(cnt + N)
-    tail_row = cache.cap + seq * cache.H * P                # after any growth
-    npf = T // P
-    dev = cache.sm.device
-    pg = _pages_arg(pages, npf + int(open_page), dev)
-    ws = torch.empty(npf * cache.H + 2, dtype=torch.int32, device=dev)
-    _lib.call("exkv_wire_unpack", _lib.ptr(blob, align=256, what="blob"), blob.numel(), _lib.ptr(cache.sm),
-              _lib.ptr(cache.code), _lib.ptr(cache.base), _lib.ptr(cache.rowmask), _lib.ptr(cache.rowoff),
-              _lib.ptr(cache.raw), cache.raw.shape[0], cache.cap, _lib.ptr(cache.cnt, align=4),
-              _lib.ptr(cache._before, align=4), _lib.ptr(pg, align=4), int(open_page), pool_pages, tail_row,
-              cache.H, T, cache.D, _lib.ptr(ws, align=4), _lib.stream())
+    infos = [_sequence(cache, s) for s in seqs]                 # tail rows after any growth
+    d, width, max_t, ws_stride = _batch_args(cache, seqs, infos, blobs, dev)
+    _lib.call("exkv_wire_unpack", _lib.ptr(cache.sm), _lib.ptr(cache.code), _lib.ptr(cache.base),
+              _lib.ptr(cache.rowmask), _lib.ptr(cache.rowoff), _lib.ptr(cache.raw), cache.raw.shape[0], cache.cap,
+              _lib.ptr(cache.cnt, align=4), _lib.ptr(cache._before, align=4), infos[0][3], len(seqs),
+              d["pages"].data_ptr(), width, d["tokens"].data_ptr(), d["open"].data_ptr(), d["tails"].data_ptr(),
+              d["blobs"].data_ptr(), d["sizes"].data_ptr(), max_t, cache.H, cache.D, d["ws"].data_ptr(), ws_stride,
+              _lib.stream())
     cache._ensure_headroom(cnt + N)

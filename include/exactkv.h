@@ -104,7 +104,7 @@ int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf,
                            int32_t H, int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
                            hipStream_t stream);
 
-/* Wire form of one sequence's compressed cache: one contiguous little-endian blob
+/* Wire form of a sequence's compressed cache: one contiguous little-endian blob
  *   header  256 B: u32 magic 0x564B5845 ("EXKV"), version 1, heads H, head_dim 128,
  *           tokens T, full_pages T/16, tail_rows T%16, raw_rows N; u64 off_tail,
  *           off_rowmask, off_base, off_sm, off_code, off_raw, total; zeros
@@ -118,25 +118,34 @@ int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf,
 /* Blob size for H heads, T tokens and N raw rows (-1 for bad arguments). */
 int64_t exkv_wire_bytes(int32_t H, int32_t T, int64_t raw_rows);
 
-/* Pack the sequence whose page p is pool page pages[p] (p < T/16; entries clamped to the
- * pool_pages pages of the arrays) and whose open page's rows are raw rows
- * tail_row + h*16 + r. ws: int32 [T/16*H + 2] scratch. blob: 256-byte aligned,
- * blob_bytes >= exkv_wire_bytes(H, T, N) for the sequence's N raw rows (rows past
- * blob_bytes are not written; the header still counts them). */
+/* Pack nseq sequences of one compressed cache (arrays as above, pool_pages pages of
+ * 16 tokens) into one blob each. Sequence s has tokens[s] (<= max_tokens) tokens; its page
+ * p is pool page pages[s * page_stride + p] (entries clamped to the pool); its open page's
+ * row r of head h is raw row tail_rows[s] + h*16 + r. blobs[s] (device address, 256-byte
+ * aligned) has blob_bytes[s] >= exkv_wire_bytes(H, tokens[s], N_s) bytes for the sequence's
+ * N_s raw rows (rows past blob_bytes[s] are not written). ws: int32 scratch
+ * [nseq, ws_stride], ws_stride >= (max_tokens/16)*H + 3. Two launches; a sequence whose
+ * tokens or blob size do not fit is skipped. */
 int exkv_wire_pack(const void* sm, const void* code, const void* base, const int32_t* rowmask,
-                   const int32_t* rowoff, const void* raw, int64_t raw_rows, const int32_t* pages,
-                   int64_t pool_pages, int64_t tail_row, int32_t H, int32_t T, int32_t D, int32_t* ws,
-                   void* blob, int64_t blob_bytes, hipStream_t stream);
+                   const int32_t* rowoff, const void* raw, int64_t raw_rows, int64_t pool_pages, int32_t nseq,
+                   const int32_t* pages, int64_t page_stride, const int32_t* tokens, const int64_t* tail_rows,
+                   const uint64_t* blobs, const int64_t* blob_bytes, int32_t max_tokens, int32_t H, int32_t D,
+                   int32_t* ws, int64_t ws_stride, hipStream_t stream);
 
-/* Unpack a blob (H, T from its header, checked by the caller) into pool pages pages[p]:
- * raw rows take slots from *cnt on (*before = old counter; slots >= cap are dropped, so
- * an overflow shows in the counter as for exkv_encode_pages), the open page's rows go
- * to raw rows tail_row + h*16 + r, and if open_page, page pages[T/16] is opened
- * (rowmask 0xFFFF, rowoff into the tail area). */
-int exkv_wire_unpack(const void* blob, int64_t blob_bytes, void* sm, void* code, void* base, int32_t* rowmask,
-                     int32_t* rowoff, void* raw, int64_t raw_rows, int64_t cap, int32_t* cnt, int32_t* before,
-                     const int32_t* pages, int32_t open_page, int64_t pool_pages, int64_t tail_row, int32_t H,
-                     int32_t T, int32_t D, int32_t* ws, hipStream_t stream);
+/* Unpack nseq blobs into sequences of a compressed cache (arguments as for exkv_wire_pack;
+ * the blob's header must give heads H, head_dim 128 and tokens[s], else it is skipped).
+ * Raw rows take pool slots from *cnt on, blob after blob, each blob's rows in its
+ * (page, head, token) order; *before = the counter before, *cnt += the rows the headers
+ * declare; slots >= cap are dropped (overflow shows in the counter, as for
+ * exkv_encode_pages). The open page's rows go to raw rows tail_rows[s] + h*16 + r (which
+ * must lie in the tail area, at or past cap), and if open[s], page
+ * pages[s * page_stride + tokens[s]/16] is opened (rowmask 0xFFFF, rowoff into the tail
+ * area). */
+int exkv_wire_unpack(void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
+                     int64_t raw_rows, int64_t cap, int32_t* cnt, int32_t* before, int64_t pool_pages, int32_t nseq,
+                     const int32_t* pages, int64_t page_stride, const int32_t* tokens, const int32_t* open,
+                     const int64_t* tail_rows, const uint64_t* blobs, const int64_t* blob_bytes,
+                     int32_t max_tokens, int32_t H, int32_t D, int32_t* ws, int64_t ws_stride, hipStream_t stream);
 
 /* Compressed cache -> bf16 out [B, T, H, 128] through the attention kernels' page decoder.
  * Replaces: kernels.py:331-337 decode_to_bf16 (_dec_only_kernel :197-211). */

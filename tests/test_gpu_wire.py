@@ -94,13 +94,17 @@ def test_paged_pack_unpack_into_another_pool():
         exactkv.check_overflow([ka, va])
     tb.release(0)
     _say("wire paged", [ta.length(s) for s in range(4)])
-    for s in (2, 0, 3, 1):                                          # slots in another order
+    order = (2, 0, 3, 1)                                            # slots in another order
+    kblobs = wire.pack_many(ka, order)                              # one call for all K
+    for s in order:
+        tb.add(ta.length(s), slot=s)
+    wire.unpack_many(kblobs, kb, order)
+    for s in order:
         T = ta.length(s)
-        d = tb.add(T, slot=s)
-        wire.unpack(wire.pack(ka, s), kb, d)
-        wire.unpack(wire.pack(va, s), vb, d)
-        kt.prefill(d, src_k[s:s + 1, :T].to(DEV).contiguous())
-        vt.prefill(d, src_v[s:s + 1, :T].to(DEV).contiguous())
+        assert same_bits(kblobs[order.index(s)], wire.pack(ka, s))  # batch == one at a time
+        wire.unpack(wire.pack(va, s), vb, s)                        # V one call per sequence
+        kt.prefill(s, src_k[s:s + 1, :T].to(DEV).contiguous())
+        vt.prefill(s, src_v[s:s + 1, :T].to(DEV).contiguous())
     for c in (kb, vb):
         dec = kernels.decode_to_bf16(c.buffers(), c.TS)
         src = src_k if c is kb else src_v

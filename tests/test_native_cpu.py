@@ -51,6 +51,11 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == 1 and b"tail area" in lib.exkv_last_error()
     rc = lib.exkv_bf16_append_paged(1, 0, 0, 1, None, 1, 1, 8, 3, 4, 2, 8, 16, 128, None)
     assert rc == 1 and b"bad shape" in lib.exkv_last_error()
+    # wire form: a scratch row too short for the longest sequence's pages; cap past the raw pool
+    rc = lib.exkv_wire_pack(1, 1, 1, 1, 1, 1, 64, 4, 2, 1, 4, 1, 1, 1, 1, 64, 8, 128, 1, 10, None)
+    assert rc == 1 and b"ws stride" in lib.exkv_last_error()
+    rc = lib.exkv_wire_unpack(1, 1, 1, 1, 1, 1, 64, 80, 1, 1, 4, 2, 1, 4, 1, None, 1, 1, 1, 64, 8, 128, 1, 35, None)
+    assert rc == 1 and b"cap" in lib.exkv_last_error()
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,expect", [

@@ -166,7 +166,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2a", choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire"])
+    ap.add_argument("--workload", default="c2a",
+                    choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -181,11 +182,12 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload in ("e2e", "c3", "c2a_paged", "wire"):
+    if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
-        return {"e2e": e2e, "c3": c3_stress, "c2a_paged": paged_c2a, "wire": wire_bench}[a.workload](a)
+        return {"e2e": e2e, "c3": c3_stress, "c2a_paged": paged_c2a, "wire": wire_bench,
+                "prefill": prefill_bench}[a.workload](a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -525,6 +527,53 @@ def c3_stress(a):
 E2E_CONFIG = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                   num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
                   rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=False)
+
+
+def prefill_bench(a):
+    """Prefill into the compressed cache on a random-init Llama-3.1-8B (c4's model): 8
+    prompts of e2e-prompt (4096) tokens, one at a time, with the write-through prefill
+    (each layer's K/V encoded straight from the attention module) and with the two-pass
+    prefill (the model's DynamicCache holds all 32 layers' K/V, then each layer is encoded).
+    Reports tokens/s and the peak memory above the weights and caches for each."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import exactkv_amd as exactkv
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    PL, NS = a.e2e_prompt, 8
+    print("[prefill] building random-init Llama-3.1-8B", file=sys.stderr, flush=True)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(LlamaConfig(**E2E_CONFIG)).to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, E2E_CONFIG["vocab_size"], (NS, PL), generator=g).to(dev)
+    eng = exactkv.Engine(model, NS, PL + 16, backend="exactkv", graph=False)
+    res = {}
+    for fused in (True, False, True):                  # warm both paths; the last run counts
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        toks = eng.prefill(ids, fused=fused)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        res[fused] = (dt, torch.cuda.max_memory_allocated() - base, toks.clone())
+        print(f"[prefill] fused={fused}: {NS * PL / dt:.0f} tok/s", file=sys.stderr, flush=True)
+    same = torch.equal(res[True][2], res[False][2])
+    tps = NS * PL / res[True][0]
+    out = {
+        "metric": "prefill tokens/s into the compressed cache (write-through), Llama-3.1-8B",
+        "value": round(tps, 1), "unit": "tok/s", "n_gpus": 1, "steps": NS, "warmup": NS,
+        "ms_per_step": round(res[True][0] / NS * 1e3, 3), "higher_is_better": True, "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "prefill: Llama-3.1-8B random init, 8 prompts x 4096 tokens, one at a time",
+                   "prompt": PL, "sequences": NS},
+        "two_pass_tok_s": round(NS * PL / res[False][0], 1),
+        "peak_extra_gib": {"write_through": round(res[True][1] / 2**30, 3), "two_pass": round(res[False][1] / 2**30, 3)},
+        "same_next_tokens": bool(same), "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(out), flush=True)
 
 
 def e2e(a):

@@ -32,6 +32,33 @@ def _fused_sdpa():
     return sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION])
 
 
+_WRITE_THROUGH = None
+
+
+def _write_through(engine, b):
+    """A prefill-only transformers cache whose update() encodes the layer's keys and values
+    into sequence slot b of the engine's caches and keeps nothing, so the model's forward
+    pass holds one layer's K/V at a time. Its layer list stays empty: the model reads a
+    sequence length of 0 and masks for the prompt alone, as for a fresh DynamicCache."""
+    global _WRITE_THROUGH
+    if _WRITE_THROUGH is None:
+        from transformers.cache_utils import DynamicCache
+
+        class WriteThrough(DynamicCache):
+            def __init__(self, eng, slot):
+                super().__init__()
+                self.eng, self.slot = eng, slot
+
+            def update(self, key_states, value_states, layer_idx, *args, **kwargs):
+                kc, vc = self.eng.kv[layer_idx]
+                kc.prefill_slot(self.slot, key_states.transpose(1, 2))     # [1, T, H, D] view, no copy
+                vc.prefill_slot(self.slot, value_states.transpose(1, 2))
+                return key_states, value_states
+
+        _WRITE_THROUGH = WriteThrough
+    return _WRITE_THROUGH(engine, b)
+
+
 class Engine:
     def __init__(self, model, B, T_max, backend="exactkv", attn=None, before_step=None, graph=True):
         """backend: 'exactkv' / 'bf16', or a cache class with the same interface.
@@ -62,6 +89,7 @@ class Engine:
         self._stream = torch.cuda.Stream(device=self.dev) if self.use_graph else None
         self._graph = None
         self._graph_key = None
+        self.captures = 0                       # HIP-graph captures of the decode step
         self._warm = False
         self._tok = torch.zeros(B, dtype=torch.long, device=self.dev)
         self._pos = torch.zeros(1, 1, dtype=torch.long, device=self.dev)
@@ -69,23 +97,33 @@ class Engine:
 
     # ---------------------------------------------------------------- prefill
     @torch.no_grad()
-    def prefill(self, ids, b0=0):
+    def prefill(self, ids, b0=0, fused=True):
         """ids: [B, T] token ids. Returns the greedy next token of each sequence, [B].
         b0 (additive): fill sequence slots b0.. with ids' rows, so a long prefill can be
-        done in pieces (slot 0 first)."""
+        done in pieces (slot 0 first).
+        fused (additive): each layer's RoPE'd keys and values go straight from the
+        attention module into the page encoder, read in place through strides ([1, H, T, D]
+        as a [1, T, H, D] view), so the model's DynamicCache never holds the prompt's K/V
+        (reference engine.py:42-49 builds it, then cache.py:87-98 copies each layer out of
+        it). fused=False keeps that order (the K/V of all layers live until the forward
+        pass ends); both give the same cache bytes."""
         nxt = []
         with _fused_sdpa():
             for i0 in range(ids.shape[0]):
                 b = b0 + i0
-                out = self.m.model(ids[i0:i0 + 1], use_cache=True)
-                pkv = out.past_key_values
-                for i in range(self.L):
-                    lay = pkv.layers[i] if hasattr(pkv, "layers") else None
-                    k, v = (lay.keys, lay.values) if lay is not None else (pkv.key_cache[i], pkv.value_cache[i])
-                    self.kv[i][0].prefill_slot(b, k.transpose(1, 2).contiguous())
-                    self.kv[i][1].prefill_slot(b, v.transpose(1, 2).contiguous())
+                if fused:
+                    out = self.m.model(ids[i0:i0 + 1], use_cache=True, past_key_values=_write_through(self, b))
+                else:
+                    out = self.m.model(ids[i0:i0 + 1], use_cache=True)
+                    pkv = out.past_key_values
+                    for i in range(self.L):
+                        lay = pkv.layers[i] if hasattr(pkv, "layers") else None
+                        k, v = (lay.keys, lay.values) if lay is not None else (pkv.key_cache[i], pkv.value_cache[i])
+                        self.kv[i][0].prefill_slot(b, k.transpose(1, 2))
+                        self.kv[i][1].prefill_slot(b, v.transpose(1, 2))
+                    del pkv
                 nxt.append(self.m.lm_head(self.m.model.norm(out.last_hidden_state[:, -1])).argmax(-1))
-                del out, pkv
+                del out
         self._graph = None                      # buffers may have grown
         return torch.cat(nxt)
 
@@ -166,6 +204,7 @@ class Engine:
                         with torch.cuda.graph(self._graph, stream=self._stream):
                             self._logits = self._forward(self._tok, device_only=True)
                         self._graph_key = key
+                        self.captures += 1
                     self._graph.replay()
                     logits = self._logits.clone()
             cur.wait_stream(self._stream)

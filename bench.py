@@ -674,17 +674,17 @@ def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table
         va, _, _, _ = kernels._cache_args(vc)
         _lib.call("exkv_attn_split_compressed_paged", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
                   wl.data_ptr(), block_table.data_ptr(), block_table.shape[1], Bp * TSp // 16, B, Hq, Hkv, D, T,
-                  block_table.shape[1] * 16, lp, lstride, ns, sl, scale, _lib.stream())
+                  block_table.shape[1] * 16, lp, lstride, ns, sl, 0, scale, _lib.stream())
         return
     if compressed:
         ka, TS, Hkv, _ = kernels._cache_args(kc)
         va, _, _, _ = kernels._cache_args(vc)
         _lib.call("exkv_attn_split_compressed", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, 0, scale, _lib.stream())
     else:
         TS, Hkv = kc.shape[1], kc.shape[2]
         _lib.call("exkv_attn_split_bf16", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, 0, scale, _lib.stream())
 
 
 def encoder_gbps(exactkv, kernels, x, T, steps, warmup):

@@ -27,21 +27,21 @@ SIGNATURES = {
     "exkv_bf16_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
-                             _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
+                             _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_attn_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
-                       _f32, _p],
+                       _i32, _f32, _p],
     "exkv_attn_split_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p,
-                                   _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _f32, _p],
+                                   _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_attn_split_bf16": [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
-                             _f32, _p],
+                             _i32, _f32, _p],
     "exkv_attn_compressed_paged": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p,
                                    _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,
-                                   _f32, _p],
+                                   _i32, _f32, _p],
     "exkv_attn_split_compressed_paged": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p,
                                          _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32,
-                                         _i32, _f32, _p],
+                                         _i32, _i32, _f32, _p],
     "exkv_attn_bf16_paged": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                             _p, _i64, _i32, _i32, _f32, _p],
+                             _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_wire_bytes": [_i32, _i32, _i64],
     "exkv_wire_pack": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i32, _i32, _i32, _p,
                        _i64, _p],

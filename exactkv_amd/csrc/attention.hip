@@ -108,6 +108,7 @@ struct AttnArgs {
     const int32_t* lens;      // per-sequence valid tokens (nullptr: T for all)
     int64_t lens_stride;
     int B, Hq, Hkv, G, HG, TS, T, nsplit, split_len;
+    int window;               // > 0: attend to the last `window` tokens of each sequence only
     int HW;                   // KV heads per workgroup (gcd(Hkv, 8)); 8 / HW page phases per head
     float qk_scale;
     uint16_t* out;            // [B, Hq, 128] bf16, written by the last workgroup of each unit
@@ -491,7 +492,9 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     const int phase = wave / a.HW, nphase = kWaves / a.HW;
     int len = a.lens ? a.lens[b * a.lens_stride] : a.T;
     len = min(max(len, 0), a.TS);
-    const int start = split * a.split_len;
+    // sliding window: tokens [lo, len) only; the splits start at lo's page
+    const int wlo = a.window > 0 ? max(len - a.window, 0) : 0;
+    const int start = (wlo & ~(kPage - 1)) + split * a.split_len;
     const int end = min(start + a.split_len, len);
     const int NP = a.TS / kPage;
 
@@ -624,8 +627,8 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         stg = stg == NST - 1 ? 0 : stg + 1;
         const int pg = p0 + phase + nphase * j;
         const int t0 = pg * kPage;
-        const bool ragged = t0 + kPage > end;          // uniform: only the last page of a split
-        const bool row_valid = t0 + r < end;
+        const bool ragged = t0 + kPage > end || t0 < wlo;  // uniform: a split's last page, or the window's first
+        const bool row_valid = t0 + r < end && t0 + r >= wlo;
         const PageMeta mc = COMP ? meta(j) : PageMeta{0u, 0u, 0, 0};
 
         // The next page's loads: the bf16 twin's at once; the compressed cache's once this
@@ -727,7 +730,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         // reads see the accumulators before the MFMA wrote them.
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = t0 + 4 * g + i < end ? sa[i] : -INFINITY;
+        for (int i = 0; i < 4; ++i) sc[i] = (t0 + 4 * g + i < end && t0 + 4 * g + i >= wlo) ? sa[i] : -INFINITY;
         float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mloc = group_max(mloc) * a.qk_scale;
         const float m_new = fmaxf(m_i, mloc);
@@ -874,20 +877,23 @@ static int heads_per_block(int Hkv) {
 }
 
 static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_t* lens, int nsplit,
-                      int split_len) {
+                      int split_len, int window) {
     EXKV_REQUIRE(D == kD, "attention: head dim must be 128 (got %d)", D);
     EXKV_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "attention: bad heads Hq=%d Hkv=%d (B=%d)", Hq,
                  Hkv, B);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "attention: TS=%d must be a positive multiple of 16", TS);
     EXKV_REQUIRE(nsplit > 0 && split_len > 0 && split_len % kPage == 0,
                  "attention: split_len=%d must be a positive multiple of 16 (nsplit=%d)", split_len, nsplit);
+    EXKV_REQUIRE(window >= 0, "attention: negative window %d", window);
+    // a sequence's splits cover [lo's page, len): at most window + 15 tokens with a window
+    const int64_t reach = window > 0 ? (int64_t)window + kPage - 1 : INT64_MAX;
     if (lens == nullptr) {
         EXKV_REQUIRE(T >= 1 && T <= TS, "attention: T=%d outside [1, TS=%d]", T, TS);
-        EXKV_REQUIRE((int64_t)nsplit * split_len >= T, "attention: %d splits of %d do not cover T=%d", nsplit,
-                     split_len, T);
+        EXKV_REQUIRE((int64_t)nsplit * split_len >= min((int64_t)T, reach),
+                     "attention: %d splits of %d do not cover T=%d (window %d)", nsplit, split_len, T, window);
     } else {
-        EXKV_REQUIRE((int64_t)nsplit * split_len >= TS,
-                     "attention: with per-sequence lengths the splits must cover TS=%d", TS);
+        EXKV_REQUIRE((int64_t)nsplit * split_len >= min((int64_t)TS, reach),
+                     "attention: with per-sequence lengths the splits must cover TS=%d (window %d)", TS, window);
     }
     EXKV_REQUIRE((int64_t)B * (Hkv / heads_per_block(Hkv)) * ((Hq / Hkv + 15) / 16) < 65536,
                  "attention: too many (sequence, head block) units");
@@ -916,8 +922,8 @@ static int fill_compressed(AttnArgs& a, const void* q, const void* k_sm, const v
                            const int32_t* v_rowoff, const void* v_raw, int64_t v_raw_rows, float* ws_o,
                            float* ws_m, float* ws_l, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T,
                            int32_t TS, const int32_t* lens, int64_t lens_stride, int32_t nsplit,
-                           int32_t split_len, float qk_scale) {
-    const int rc = check_attn(B, Hq, Hkv, D, T, TS, lens, nsplit, split_len);
+                           int32_t split_len, int32_t window, float qk_scale) {
+    const int rc = check_attn(B, Hq, Hkv, D, T, TS, lens, nsplit, split_len, window);
     if (rc) return rc;
     EXKV_REQUIRE(k_raw_rows > 0 && v_raw_rows > 0, "attn_compressed: empty raw pool");
     EXKV_REQUIRE(q && k_sm && k_code && k_base && k_rowmask && k_rowoff && k_raw && v_sm && v_code && v_base &&
@@ -932,14 +938,16 @@ static int fill_compressed(AttnArgs& a, const void* q, const void* k_sm, const v
     a.part_o = ws_o; a.part_m = ws_m; a.part_l = ws_l;
     a.lens = lens; a.lens_stride = lens_stride;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
-    a.nsplit = nsplit; a.split_len = split_len; a.qk_scale = qk_scale; a.HW = heads_per_block(Hkv);
+    a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
+    a.HW = heads_per_block(Hkv);
     return EXKV_OK;
 }
 
 static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, float* ws_o, float* ws_m,
                      float* ws_l, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
-                     const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len, float qk_scale) {
-    const int rc = check_attn(B, Hq, Hkv, D, T, TS, lens, nsplit, split_len);
+                     const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len, int32_t window,
+                     float qk_scale) {
+    const int rc = check_attn(B, Hq, Hkv, D, T, TS, lens, nsplit, split_len, window);
     if (rc) return rc;
     EXKV_REQUIRE(q && k && v && ws_o && ws_m && ws_l, "attn_bf16: null pointer");
     a = AttnArgs{};
@@ -948,7 +956,8 @@ static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, f
     a.part_o = ws_o; a.part_m = ws_m; a.part_l = ws_l;
     a.lens = lens; a.lens_stride = lens_stride;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
-    a.nsplit = nsplit; a.split_len = split_len; a.qk_scale = qk_scale; a.HW = heads_per_block(Hkv);
+    a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
+    a.HW = heads_per_block(Hkv);
     return EXKV_OK;
 }
 
@@ -962,8 +971,8 @@ static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, f
         v_raw, v_raw_rows, ws_o, ws_m, ws_l
 #define EXKV_SHAPE_PARAMS                                                                                  \
     int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t *lens, int64_t lens_stride, \
-        int32_t nsplit, int32_t split_len, float qk_scale
-#define EXKV_SHAPE_ARGS B, Hq, Hkv, D, T, TS, lens, lens_stride, nsplit, split_len, qk_scale
+        int32_t nsplit, int32_t split_len, int32_t window, float qk_scale
+#define EXKV_SHAPE_ARGS B, Hq, Hkv, D, T, TS, lens, lens_stride, nsplit, split_len, window, qk_scale
 
 extern "C" int exkv_attn_compressed(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, EXKV_SHAPE_PARAMS,
                                     hipStream_t stream) {

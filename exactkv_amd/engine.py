@@ -71,7 +71,13 @@ class Engine:
         self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.Hq
         assert cfg.model_type in ("qwen2", "qwen3", "llama"), \
             f"supported: Qwen2/2.5, Qwen3, Llama-3 (got {cfg.model_type})"
-        assert not getattr(cfg, "use_sliding_window", False), "sliding-window attention is not supported"
+        # sliding-window layers (Qwen2/Qwen3 use_sliding_window; not supported by the reference,
+        # engine.py:26-28): decode attention reads each sequence's last `sliding_window`
+        # tokens, the keys the model's own mask admits (positions > p - window)
+        sw = getattr(cfg, "sliding_window", None) if getattr(cfg, "use_sliding_window", False) else None
+        kinds = getattr(cfg, "layer_types", None) or ["full_attention"] * self.L
+        self.windows = [int(sw) if sw and kinds[i] == "sliding_attention" else 0 for i in range(self.L)]
+        assert attn is None or not any(self.windows), "attention plug-ins do not take a sliding window"
         assert self.D == 128, "head dim 128 only"
         self.B, self.TS = B, -(-T_max // P) * P
         self.dev = next(model.parameters()).device
@@ -128,13 +134,13 @@ class Engine:
         return torch.cat(nxt)
 
     # ---------------------------------------------------------------- decode step
-    def _attend(self, q, kc, vc):
+    def _attend(self, q, kc, vc, window=0):
         if self.attn is not None:
             return self.attn(q, kc, vc)
         lens = kc.state[:1]                     # token count on the device (after this step's append)
         if isinstance(kc, CompressedKV):
-            return attention_compressed(q, kc, vc, kc.TS, lens=lens)
-        return attention_reference(q, kc.buf, vc.buf, kc.TS, lens=lens)
+            return attention_compressed(q, kc, vc, kc.TS, lens=lens, window=window)
+        return attention_reference(q, kc.buf, vc.buf, kc.TS, lens=lens, window=window)
 
     def _forward(self, tok, device_only):
         """One decode step: tok [B] -> logits [B, vocab]. device_only: appends launch their
@@ -164,7 +170,7 @@ class Engine:
             else:
                 kc.append(k[:, :, 0])
                 vc.append(v[:, 0])
-            o = self._attend(q[:, :, 0].contiguous(), kc, vc)
+            o = self._attend(q[:, :, 0].contiguous(), kc, vc, self.windows[i])
             h = h + att.o_proj(o.reshape(B, 1, Hq * D))
             h = h + layer.mlp(layer.post_attention_layernorm(h))
         return m.lm_head(m.model.norm(h))[:, 0]

@@ -113,10 +113,20 @@ def _cache_args(c):
     return (*ptrs, raw.shape[0]), TS, H, B
 
 
-def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len):
+def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window=0):
     if nsplit is not None and split_len is not None:
         return nsplit, split_len
-    return plan_splits(B, Hkv, Hq, TS if lens is not None else T)
+    reach = TS if lens is not None else T
+    if window:                                 # the splits start at the window's first page
+        reach = min(reach, window + P - 1)
+    return plan_splits(B, Hkv, Hq, reach)
+
+
+def _window_arg(window):
+    w = int(window or 0)
+    if w < 0:
+        raise ValueError(f"window must be >= 0 (got {w})")
+    return w
 
 
 def _lens_arg(lens, B):
@@ -140,14 +150,17 @@ def _block_table_arg(block_table, B):
 
 
 def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                         split_len=None, out=None, fused_merge=False, block_table=None):
+                         split_len=None, out=None, fused_merge=False, block_table=None, window=0):
     """q [B, Hq, 128] bf16 contiguous; kc, vc: CompressedKV objects (or their .buffers()
     dicts); T: valid tokens. Returns bf16 [B, Hq, 128], bit-identical to
     attention_reference on the same contents and split plan.
 
     block_table (int32 [B, max_pages], on the GPU): paged caches. kc / vc are then pools
     of pages (any [Bp, TSp] shape, read as Bp * TSp / 16 pages in order) and page p of
-    sequence b is pool page block_table[b, p]; T / lens count tokens of the sequences."""
+    sequence b is pool page block_table[b, p]; T / lens count tokens of the sequences.
+
+    window > 0 (sliding-window attention; not in the reference, engine.py:26-28 rejects
+    it): each sequence attends to its last `window` tokens only."""
     _check_q(q)
     ka, TS, Hkv, Bc = _cache_args(kc)
     va, TSv, Hv, Bv = _cache_args(vc)
@@ -158,7 +171,8 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
         bt, bts, cap = _block_table_arg(block_table, B)
         pool_pages = Bc * TS // P
         TS = cap
-    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
+    window = _window_arg(window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
@@ -166,16 +180,16 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     if block_table is not None:
         _lib.call("exkv_attn_compressed_paged", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
                   cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B, Hq, Hkv, D,
-                  int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+                  int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream())
         return out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
-              cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E,
+              cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E,
               _lib.stream())
     return out
 
 
 def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
-                        split_len=None, out=None, fused_merge=False, block_table=None):
+                        split_len=None, out=None, fused_merge=False, block_table=None, window=0):
     """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous);
     with block_table, k and v are pools of pages as in attention_compressed."""
     _check_q(q)
@@ -191,7 +205,8 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
         bt, bts, cap = _block_table_arg(block_table, B)
         pool_pages = k.shape[0] * TS // P
         TS = cap
-    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len)
+    window = _window_arg(window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
     wo, wm, wl = _workspace(q.device, B * Hq, ns)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
@@ -199,10 +214,10 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     if block_table is not None:
         _lib.call("exkv_attn_bf16_paged", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
                   wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B,
-                  Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, D ** -0.5 * LOG2E, _lib.stream())
+                  Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream())
         return out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
-              wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl,
+              wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window,
               D ** -0.5 * LOG2E, _lib.stream())
     return out
 

@@ -162,6 +162,10 @@ int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, cons
  * workspace must not overlap.
  * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
  * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
+ * window > 0 (sliding-window attention): only the last `window` of those tokens,
+ * [len - window, len); the splits then start at that range's first page, so they need
+ * to cover only min(T or TS, window + 15) tokens. window = 0: all tokens. (Additive: the
+ * reference has no window, engine.py:26-28.)
  * qk_scale = 128^-1/2 * log2(e). Bit-identical to exkv_attn_bf16 on the decoded contents.
  * Replaces: kernels.py:310-318 attention_compressed (_split_c_kernel :142-165 and
  * _reduce_kernel :33-43). */
@@ -172,14 +176,14 @@ int exkv_attn_compressed(const void* q, const void* k_sm, const void* k_code, co
                          int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, int32_t* ws_cnt, void* out,
                          int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                          const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
-                         float qk_scale, hipStream_t stream);
+                         int32_t window, float qk_scale, hipStream_t stream);
 
 /* The same attention over plain bf16 caches k, v [B, TS, Hkv, 128].
  * Replaces: kernels.py:321-328 attention_reference (_split_ref_kernel :168-194). */
 int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
                    int32_t* ws_cnt, void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                    const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
-                   float qk_scale, hipStream_t stream);
+                   int32_t window, float qk_scale, hipStream_t stream);
 
 /* The two phases of exkv_attn_compressed / exkv_attn_bf16 separately: the split kernel
  * (partials into ws_o, ws_m, ws_l) and the merge of `nsplit` partials per row into
@@ -192,12 +196,12 @@ int exkv_attn_split_compressed(const void* q, const void* k_sm, const void* k_co
                                const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
                                int64_t v_raw_rows, float* ws_o, float* ws_m, float* ws_l, int32_t B,
                                int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t* lens,
-                               int64_t lens_stride, int32_t nsplit, int32_t split_len, float qk_scale,
+                               int64_t lens_stride, int32_t nsplit, int32_t split_len, int32_t window, float qk_scale,
                                hipStream_t stream);
 int exkv_attn_split_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
                          int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                          const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
-                         float qk_scale, hipStream_t stream);
+                         int32_t window, float qk_scale, hipStream_t stream);
 int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, void* out, int64_t rows,
                      int32_t nsplit, int32_t D, hipStream_t stream);
 
@@ -216,7 +220,7 @@ int exkv_attn_compressed_paged(const void* q, const void* k_sm, const void* k_co
                                void* out, const int32_t* block_table, int64_t bt_stride, int32_t pool_pages,
                                int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                                const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
-                               float qk_scale, hipStream_t stream);
+                               int32_t window, float qk_scale, hipStream_t stream);
 int exkv_attn_split_compressed_paged(const void* q, const void* k_sm, const void* k_code, const void* k_base,
                                      const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
                                      int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
@@ -225,12 +229,12 @@ int exkv_attn_split_compressed_paged(const void* q, const void* k_sm, const void
                                      const int32_t* block_table, int64_t bt_stride, int32_t pool_pages, int32_t B,
                                      int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                                      const int32_t* lens, int64_t lens_stride, int32_t nsplit,
-                                     int32_t split_len, float qk_scale, hipStream_t stream);
+                                     int32_t split_len, int32_t window, float qk_scale, hipStream_t stream);
 int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
                          int32_t* ws_cnt, void* out, const int32_t* block_table, int64_t bt_stride,
                          int32_t pool_pages, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
                          const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
-                         float qk_scale, hipStream_t stream);
+                         int32_t window, float qk_scale, hipStream_t stream);
 
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
  * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 64), split_len a multiple of 32.

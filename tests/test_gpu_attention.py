@@ -151,3 +151,71 @@ def test_bad_arguments_raise():
         kernels.attention_reference(q, k, k, 33)
     with pytest.raises(ValueError):
         kernels.attention_reference(q.float(), k, k, 3)
+
+
+def _window_oracle(q, k, v, lens, W):
+    """fp32 oracle over tokens [len - W, len) of each sequence."""
+    outs = []
+    for b, n in enumerate(lens):
+        lo = max(n - W, 0)
+        outs.append(oatt.attention(u16(q[b:b + 1]), u16(k[b:b + 1, lo:n]), u16(v[b:b + 1, lo:n]), n - lo,
+                                   np.float32))
+    return np.concatenate(outs)
+
+
+@pytest.mark.parametrize("W", [1, 7, 16, 40, 333, 4096])
+def test_sliding_window(W):
+    """window > 0: each sequence attends to its last W tokens (no reference counterpart;
+    its engine rejects sliding-window models, engine.py:26-28). Compressed == twin bit for
+    bit, within the north-star tolerance of the oracle over the window, and equal to the
+    full attention of a cache that holds only the window's tokens."""
+    B, TS, Hq, Hkv = 3, 1024, 32, 8
+    lens = [1000, 517, 33]
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=71, raw_row_rate=0.01)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=72, raw_row_rate=0.01)
+    q = synthetic.make_q(B, Hq, seed=73)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    ld = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    _say("window", W, lens)
+    o_c = kernels.attention_compressed(qd, kc, vc, 0, lens=ld, window=W)
+    o_r = kernels.attention_reference(qd, kd, vd, 0, lens=ld, window=W)
+    assert same_bits(o_c, o_r)
+    assert_bf16_tolerance(o_c, _window_oracle(q, k, v, lens, W))
+    if W >= TS:                                       # a window longer than every sequence: no change
+        assert same_bits(o_c, kernels.attention_compressed(qd, kc, vc, 0, lens=ld))
+    # one length for all (no lens), several split plans
+    T = 700
+    for ns, sl in ((None, None), (1, -(-min(T, W + 15) // 32) * 32), (None, 64)):
+        if sl is not None and ns is None:
+            ns = -(-min(T, W + 15) // sl)
+        o1 = kernels.attention_compressed(qd, kc, vc, T, window=W, nsplit=ns, split_len=sl)
+        assert same_bits(o1, kernels.attention_reference(qd, kd, vd, T, window=W, nsplit=ns, split_len=sl))
+        assert_bf16_tolerance(o1, _window_oracle(q, k, v, [T] * B, W))
+
+
+def test_sliding_window_paged_and_bad_arguments():
+    B, Hq, Hkv, npg, W = 2, 32, 8, 20, 100
+    pool_pages = 48
+    base = synthetic.make_kv(1, pool_pages * 16, Hkv, kind="k", seed=81)
+    vbase = synthetic.make_kv(1, pool_pages * 16, Hkv, kind="v", seed=82)
+    table = torch.randperm(pool_pages, generator=torch.Generator().manual_seed(4))[:B * npg].view(B, npg)
+    table = table.to(torch.int32)
+    q = synthetic.make_q(B, Hq, seed=83)
+    kd, vd, qd = base.to(DEV), vbase.to(DEV), q.to(DEV)
+    kpc, vpc = _encode(kd), _encode(vd)
+    idx = (table.long()[:, :, None] * 16 + torch.arange(16)[None, None, :]).reshape(B, npg * 16)
+    kg, vg = base[0][idx], vbase[0][idx]
+    T = npg * 16 - 9
+    bt = table.to(DEV)
+    _say("window paged", W, T)
+    o_p = kernels.attention_compressed(qd, kpc, vpc, T, block_table=bt, window=W)
+    o_g = kernels.attention_reference(qd, kg.to(DEV).contiguous(), vg.to(DEV).contiguous(), T, window=W)
+    assert same_bits(o_p, o_g)
+    assert_bf16_tolerance(o_p, _window_oracle(q, kg, vg, [T] * B, W))
+    q1 = qd[:1].contiguous()
+    with pytest.raises(ValueError, match="window"):
+        kernels.attention_reference(q1, kd, vd, 16, window=-1)
+    with pytest.raises(RuntimeError, match="cover"):
+        kernels.attention_reference(q1, kd[:, :512].contiguous(), vd[:, :512].contiguous(), 500, window=200,
+                                    nsplit=1, split_len=192)

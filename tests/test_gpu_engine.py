@@ -141,3 +141,43 @@ def test_fused_prefill_writes_the_same_cache(kind):
     for (ka, va), (kf, vf) in zip(ba.kv, bf.kv):
         assert torch.equal(ka.buf.view(torch.int16), kf.buf.view(torch.int16))
         assert torch.equal(va.buf.view(torch.int16), vf.buf.view(torch.int16))
+
+
+def test_sliding_window_model():
+    """Qwen2 with sliding-window layers (use_sliding_window, window 24 < the 37-token
+    prompt): both backends give bit-identical logits, and with teacher forcing they follow
+    the model's own full forward pass (its sliding-window mask) within bf16 noise, much
+    closer than the same engine with the window switched off."""
+    import exactkv_amd as exactkv
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    cfg = Qwen2Config(vocab_size=1024, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=4096, rope_theta=1e6,
+                      use_sliding_window=True, sliding_window=24, max_window_layers=0)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        m = Qwen2ForCausalLM(cfg)
+    m = m.to(torch.bfloat16).eval()
+    N = 24
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, 1024, (B, PROMPT + N + 1), generator=g).cuda()
+    with torch.no_grad():
+        ref = m(ids).logits.float()                    # the model's own masks, all positions
+    out = {}
+    for name, backend, windows in (("c", "exactkv", None), ("b", "bf16", None), ("off", "exactkv", [0, 0])):
+        eng = exactkv.Engine(m, B, PROMPT + N, backend=backend)
+        assert eng.windows == [24, 24]
+        if windows is not None:
+            eng.windows = windows
+        print(f"[engine] window {name}", flush=True)
+        eng.prefill(ids[:, :PROMPT])
+        ls = [eng.step(ids[:, PROMPT + t]).float() for t in range(N)]
+        out[name] = torch.stack(ls, 1)                 # logits at positions PROMPT + t
+    torch.cuda.synchronize()
+    assert torch.equal(out["c"], out["b"])
+    want = ref[:, PROMPT:PROMPT + N]
+    scale = want.abs().max().item()
+    err_on = (out["c"] - want).abs().max().item()
+    err_off = (out["off"] - want).abs().max().item()
+    print(f"[engine] window: err {err_on:.4g}, without the window {err_off:.4g}, scale {scale:.4g}", flush=True)
+    assert err_on <= 0.03 * scale
+    assert err_off > 4 * err_on

@@ -60,22 +60,24 @@ def cpu_model():
     return platform.processor()
 
 
-def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None):
+def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0):
     """Bytes a decode-attention call must move: per K/V cache and valid token row
     128 (sm) + 64 (code); per touched page and head 128 (base) + 8 (rowmask, rowoff);
-    256 per raw row referenced; plus q and the output. lens: per-sequence lengths."""
+    256 per raw row referenced; plus q and the output. lens: per-sequence lengths;
+    window: only each sequence's last `window` tokens count."""
     import torch
     lens = [T] * B if lens is None else [int(x) for x in lens]
     total = 0
     for c in caches:
         for b, L in enumerate(lens):
-            npg = -(-L // 16)
-            rm = c.rowmask[b, :npg].to(torch.int64)                        # [npg, Hkv]
+            lo = max(L - window, 0) if window else 0
+            p0, npg = lo // 16, -(-L // 16)
+            rm = c.rowmask[b, p0:npg].to(torch.int64)                       # [pages, Hkv]
             bit = torch.arange(16, device=rm.device)
-            tok = torch.arange(npg, device=rm.device)[:, None] * 16 + bit     # [npg, 16]
-            raw = (rm[:, :, None] >> bit) & 1                                 # [npg, Hkv, 16]
-            raw_rows = int((raw * (tok < L)[:, None, :]).sum().item())
-            total += L * Hkv * 192 + npg * Hkv * 136 + raw_rows * 256
+            tok = torch.arange(p0, npg, device=rm.device)[:, None] * 16 + bit   # [pages, 16]
+            raw = (rm[:, :, None] >> bit) & 1                                 # [pages, Hkv, 16]
+            raw_rows = int((raw * ((tok < L) & (tok >= lo))[:, None, :]).sum().item())
+            total += (L - lo) * Hkv * 192 + (npg - p0) * Hkv * 136 + raw_rows * 256
     return total + 2 * B * Hq * 128 * 2
 
 
@@ -178,6 +180,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="minimum CPU work of the baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--target-blocks", type=int, default=None)
+    ap.add_argument("--window", type=int, default=0,
+                    help="sliding-window attention over each sequence's last WINDOW tokens (0: all)")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
@@ -219,44 +223,46 @@ def main():
     del k, v
     torch.cuda.synchronize()
     print("[bench] caches encoded", file=sys.stderr, flush=True)
-    ns, sl = kernels.plan_splits(B, Hkv, Hq, T, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
+    W = a.window
+    reach = min(T, W + 15) if W else T                 # the splits start at the window's first page
+    ns, sl = kernels.plan_splits(B, Hkv, Hq, reach, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
     out = torch.empty_like(q)
     if a.profile:
         profile_run(kernels, q, kcs[0], vcs[0], kbs[0], vbs[0], T, ns, sl, out)
         return
-    o_c = kernels.attention_compressed(q, kcs[0], vcs[0], T, nsplit=ns, split_len=sl)
-    o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl)
+    o_c = kernels.attention_compressed(q, kcs[0], vcs[0], T, nsplit=ns, split_len=sl, window=W)
+    o_r = kernels.attention_reference(q, kbs[0], vbs[0], T, nsplit=ns, split_len=sl, window=W)
     identical = torch.equal(o_c.view(torch.int16), o_r.view(torch.int16))
 
     def full_c(i):
-        kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl, out=out)
+        kernels.attention_compressed(q, kcs[i], vcs[i], T, nsplit=ns, split_len=sl, out=out, window=W)
 
     def full_b(i):
-        kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out)
+        kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out, window=W)
 
     ms_c = time_loop(full_c, a.steps, a.warmup, a.copies)
     ms_b = time_loop(full_b, a.steps, a.warmup, a.copies)
-    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True), a.steps, a.warmup,
-                         a.copies)
-    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False), a.steps,
+    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True, window=W), a.steps,
+                         a.warmup, a.copies)
+    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False, window=W), a.steps,
                            a.warmup, a.copies)
     ms_c_graph = time_graph(full_c, a.steps, a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
 
-    alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv)
-    alg_b = 2 * B * T * Hkv * 256 + 2 * B * Hq * 128 * 2
+    alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv, window=W)
+    alg_b = 2 * B * min(T, W or T) * Hkv * 256 + 2 * B * Hq * 128 * 2
     gbps = alg / (ms_split * 1e-3) / 1e9
     enc = encoder_gbps(exactkv, kernels, kbs[0], T, a.steps, a.warmup)
     print("[bench] encoder timed", file=sys.stderr, flush=True)
 
-    traffic, traffic_src = profiled_traffic(a.workload)
+    traffic, traffic_src = profiled_traffic(a.workload) if not W else (None, None)
     res = {
         "metric": METRIC, "value": round(ms_c * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_c, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{a.workload}: {desc}", "B": B, "T": T, "TS": TS, "Hq": Hq, "Hkv": Hkv,
                    "head_dim": 128, "page": 16, "nsplit": ns, "split_len": sl, "cache_copies": a.copies,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", **({"window": W} if W else {})},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
@@ -272,7 +278,7 @@ def main():
         "encoder_GBps": enc,
         "gpu": torch.cuda.get_device_name(0),
     }
-    if not a.no_cpu_baseline:
+    if not a.no_cpu_baseline and not W:                # the baseline is the full-context attention
         res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, min(a.cpu_seqs, B), a.cpu_seconds)
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
@@ -662,7 +668,7 @@ def e2e(a):
     print(json.dumps(res), flush=True)
 
 
-def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table=None):
+def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table=None, window=0):
     """Launch only the split kernel (the dominant kernel) into the shared workspace."""
     from exactkv_amd import _lib
     B, Hq, D = q.shape
@@ -674,17 +680,17 @@ def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table
         va, _, _, _ = kernels._cache_args(vc)
         _lib.call("exkv_attn_split_compressed_paged", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
                   wl.data_ptr(), block_table.data_ptr(), block_table.shape[1], Bp * TSp // 16, B, Hq, Hkv, D, T,
-                  block_table.shape[1] * 16, lp, lstride, ns, sl, 0, scale, _lib.stream())
+                  block_table.shape[1] * 16, lp, lstride, ns, sl, window, scale, _lib.stream())
         return
     if compressed:
         ka, TS, Hkv, _ = kernels._cache_args(kc)
         va, _, _, _ = kernels._cache_args(vc)
         _lib.call("exkv_attn_split_compressed", q.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, 0, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, window, scale, _lib.stream())
     else:
         TS, Hkv = kc.shape[1], kc.shape[2]
         _lib.call("exkv_attn_split_bf16", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), wo.data_ptr(), wm.data_ptr(),
-                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, 0, scale, _lib.stream())
+                  wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, window, scale, _lib.stream())
 
 
 def encoder_gbps(exactkv, kernels, x, T, steps, warmup):

@@ -98,6 +98,24 @@ def time_loop(fn, n, warmup, copies):
     return e0.elapsed_time(e1) / n
 
 
+def time_calls(fn, n, warmup, copies):
+    """Per-call times (ms): an event before each call and after the last, all on the launch
+    stream; returns (median, p10, p90)."""
+    import torch
+    for i in range(warmup):
+        fn(i % copies)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    for i in range(n):
+        ev[i].record(s)
+        fn(i % copies)
+    ev[n].record(s)
+    torch.cuda.synchronize()
+    t = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(n))
+    return t[n // 2], t[n // 10], t[(9 * n) // 10]
+
+
 def time_graph(fn, n, warmup, copies, per_graph=20):
     """Average ms per call of fn(i) with the calls captured in a HIP graph (per_graph calls
     rotating over `copies` inputs) and the graph replayed until n calls ran: the launch
@@ -247,6 +265,7 @@ def main():
     ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False, window=W), a.steps,
                            a.warmup, a.copies)
     ms_c_graph = time_graph(full_c, a.steps, a.warmup, a.copies)
+    med, p10, p90 = time_calls(full_c, max(a.steps, 50), a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
 
     alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv, window=W)
@@ -269,6 +288,8 @@ def main():
                      "kernel_us": round(ms_split * 1e3, 2)},
         "timing": "HIP events around back-to-back calls on one stream",
         "graph_replay_us": round(ms_c_graph * 1e3, 2),
+        "per_call_us": {"median": round(med * 1e3, 2), "p10": round(p10 * 1e3, 2), "p90": round(p90 * 1e3, 2),
+                        "calls": max(a.steps, 50)},
         "bf16_twin_us": round(ms_b * 1e3, 2),
         "bf16_split_us": round(ms_split_b * 1e3, 2),
         "bf16_split_GBps": round(alg_b / (ms_split_b * 1e-3) / 1e9, 1),

@@ -12,9 +12,9 @@ from .kernels import attention_compressed, attention_reference, decode_to_bf16, 
 
 
 def __getattr__(name):
-    if name == "Engine":                 # imports transformers-side helpers lazily
-        from .engine import Engine
-        return Engine
+    if name in ("Engine", "PagedEngine"):   # imports transformers-side helpers lazily
+        from . import engine
+        return getattr(engine, name)
     raise AttributeError(name)
 
 
@@ -22,4 +22,4 @@ __version__ = "0.1.0"
 __all__ = ["CompressedKV", "BF16KV", "check_overflow", "decode_attention", "Engine",
            "encode_reference", "decode_reference", "bits_per_value",
            "attention_compressed", "attention_reference", "decode_to_bf16", "encode_pages",
-           "PageTable", "PagedCompressedKV", "PagedBF16KV"]
+           "PageTable", "PagedCompressedKV", "PagedBF16KV", "PagedEngine"]

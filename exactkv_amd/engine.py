@@ -20,6 +20,7 @@ import importlib
 import torch
 
 from .cache import BF16KV, CompressedKV, check_overflow
+from .attention import decode_attention
 from .kernels import attention_compressed, attention_reference, P
 
 BACKENDS = {"exactkv": CompressedKV, "bf16": BF16KV}
@@ -33,6 +34,18 @@ def _fused_sdpa():
 
 
 _WRITE_THROUGH = None
+
+
+def _project(eng, att, x, B, cos, sin):
+    """One token's q [B, Hq, 1, D] (RoPE'd), k [B, Hkv, 1, D] (RoPE'd) and v [B, 1, Hkv, D]
+    through the model's own attention projections (Qwen3: with its q/k norms)."""
+    q = att.q_proj(x).view(B, 1, eng.Hq, eng.D)
+    k = att.k_proj(x).view(B, 1, eng.Hkv, eng.D)
+    v = att.v_proj(x).view(B, 1, eng.Hkv, eng.D)
+    if eng.qk_norm:
+        q, k = att.q_norm(q), att.k_norm(k)
+    q, k = eng.rope(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+    return q, k, v
 
 
 def _write_through(engine, b):
@@ -154,13 +167,7 @@ class Engine:
         cos, sin = m.model.rotary_emb(h, self._pos)
         for i, layer in enumerate(m.model.layers):
             att = layer.self_attn
-            x = layer.input_layernorm(h)
-            q = att.q_proj(x).view(B, 1, Hq, D)
-            k = att.k_proj(x).view(B, 1, Hkv, D)
-            v = att.v_proj(x).view(B, 1, Hkv, D)
-            if self.qk_norm:
-                q, k = att.q_norm(q), att.k_norm(k)
-            q, k = self.rope(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+            q, k, v = _project(self, att, layer.input_layernorm(h), B, cos, sin)
             kc, vc = self.kv[i]
             if device_only:
                 kc._check_token(k[:, :, 0])
@@ -230,6 +237,77 @@ class Engine:
             t = lg.argmax(-1)
             toks.append(t)
         return torch.stack(toks, 1), torch.stack(logits, 1)
+
+    def kv_bytes(self):
+        return sum(c.nbytes() for kv in self.kv for c in kv)
+
+
+class PagedEngine:
+    """Greedy decoding over paged caches: sequences of different lengths share one pool of
+    16-token pages through a PageTable, join with add() and leave with release().
+
+    No counterpart in the reference, whose engine keeps every sequence at one length in
+    contiguous caches (engine.py:18-95); paged KV is its future work (README.md:121-123).
+    The model, projections, write-through prefill and sliding-window handling are the
+    Engine's. Steps run eagerly: the block table and lengths change on the host between
+    steps (begin_step claims a page whenever a token fills one)."""
+
+    def __init__(self, model, max_seqs, T_max, backend="exactkv", num_pages=None):
+        from .paged import PageTable, PagedBF16KV, PagedCompressedKV
+        cfg = model.config
+        self.m = model
+        self.L, self.Hq, self.Hkv = cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads
+        self.D = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.Hq
+        assert cfg.model_type in ("qwen2", "qwen3", "llama"), \
+            f"supported: Qwen2/2.5, Qwen3, Llama-3 (got {cfg.model_type})"
+        assert self.D == 128, "head dim 128 only"
+        sw = getattr(cfg, "sliding_window", None) if getattr(cfg, "use_sliding_window", False) else None
+        kinds = getattr(cfg, "layer_types", None) or ["full_attention"] * self.L
+        self.windows = [int(sw) if sw and kinds[i] == "sliding_attention" else 0 for i in range(self.L)]
+        self.dev = next(model.parameters()).device
+        max_pages = -(-T_max // P)
+        self.table = PageTable(num_pages or max_seqs * max_pages, max_seqs, max_pages, device=self.dev)
+        cls = {"exactkv": PagedCompressedKV, "bf16": PagedBF16KV}[backend]
+        self.kv = [(cls(self.table, self.Hkv), cls(self.table, self.Hkv)) for _ in range(self.L)]
+        self.rope = importlib.import_module(type(model.model.layers[0].self_attn).__module__).apply_rotary_pos_emb
+        self.qk_norm = hasattr(model.model.layers[0].self_attn, "k_norm")
+        self.grows = 0
+
+    @torch.no_grad()
+    def add(self, ids, slot=None):
+        """Prefill one prompt (1-D token ids) into a new sequence slot. Returns (slot, the
+        greedy next token)."""
+        s = self.table.add(int(ids.numel()), slot)
+        with _fused_sdpa():
+            out = self.m.model(ids.view(1, -1), use_cache=True, past_key_values=_write_through(self, s))
+        return s, self.m.lm_head(self.m.model.norm(out.last_hidden_state[:, -1])).argmax(-1)[0]
+
+    def release(self, slot):
+        self.table.release(slot)
+
+    @torch.no_grad()
+    def step(self, tok, slots=None):
+        """tok: [n] the current token of each slot in `slots` (default: every live slot, in
+        order). Returns logits [n, vocab] for their next tokens."""
+        m = self.m
+        slots = self.table.begin_step(slots)
+        n = len(slots)
+        _, _, lens = self.table.step_rows()
+        pos = (lens - 1).view(n, 1).long()                                   # each sequence's position
+        h = m.model.embed_tokens(tok.view(n, 1))
+        cos, sin = m.model.rotary_emb(h, pos)
+        for i, layer in enumerate(m.model.layers):
+            att = layer.self_attn
+            q, k, v = _project(self, att, layer.input_layernorm(h), n, cos, sin)
+            kc, vc = self.kv[i]
+            kc.append(k[:, :, 0])
+            vc.append(v[:, 0])
+            o = decode_attention(q[:, :, 0].contiguous(), kc, vc, window=self.windows[i])
+            h = h + att.o_proj(o.reshape(n, 1, self.Hq * self.D))
+            h = h + layer.mlp(layer.post_attention_layernorm(h))
+        if self.table.filled_in_step():
+            self.grows += check_overflow([c for kv in self.kv for c in kv])
+        return m.lm_head(m.model.norm(h))[:, 0]
 
     def kv_bytes(self):
         return sum(c.nbytes() for kv in self.kv for c in kv)

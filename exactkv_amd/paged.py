@@ -243,6 +243,8 @@ class PagedCompressedKV:
             self._tail(slot)[:, : T - Tf] = x[0, Tf:].transpose(0, 1)
         self._ensure_headroom(n)
 
+    prefill_slot = prefill                     # the write-through prefill calls this name
+
     def append(self, x):
         """x: [n, H, D] bf16, row i the new token of the current step's slot i (begin_step)."""
         t = self.table
@@ -328,6 +330,9 @@ class PagedBF16KV:
             pages = torch.tensor(self.table._pages[slot], dtype=torch.int64)
             rows = (pages[:, None] * P + torch.arange(P)[None, :]).reshape(-1)[:T]
             self.buf[0].index_copy_(0, rows.to(self.buf.device), x[0])
+
+    def prefill_slot(self, slot, x):
+        self.prefill(slot, x)
 
     def append(self, x):
         t = self.table

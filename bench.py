@@ -187,7 +187,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2a",
-                    choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill"])
+                    choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill", "e2e_paged"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -204,12 +204,12 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill"):
+    if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
         return {"e2e": e2e, "c3": c3_stress, "c2a_paged": paged_c2a, "wire": wire_bench,
-                "prefill": prefill_bench}[a.workload](a)
+                "prefill": prefill_bench, "e2e_paged": e2e_paged}[a.workload](a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -601,6 +601,74 @@ def prefill_bench(a):
         "same_next_tokens": bool(same), "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)
+
+
+def e2e_paged(a):
+    """Greedy decoding of prompts of mixed lengths (U[1024, 4096], seeded) over a page pool
+    (PagedEngine) on the c4 model: the pool takes the KV budget of the e2e protocol and
+    admits sequences by the pages they need, where a contiguous cache reserves the longest
+    prompt + generation for every sequence. Reports how many sequences each layout fits and
+    the paged engine's decode tok/s (eager steps) at its batch."""
+    import numpy as np
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import exactkv_amd as exactkv
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    G, LMAX = 64, 4096
+    print("[e2e_paged] building random-init Llama-3.1-8B", file=sys.stderr, flush=True)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(LlamaConfig(**E2E_CONFIG)).to(torch.bfloat16).eval()
+    torch.cuda.empty_cache()
+    budget = torch.cuda.mem_get_info()[0] - 1.6 * 2**30 - a.e2e_work_gib * 2**30
+    cfg = E2E_CONFIG
+    L, H = cfg["num_hidden_layers"], cfg["num_key_value_heads"]
+    page_bytes = 2 * L * (16 * H * 192 + H * 136)                     # K and V of all layers, one page
+    per_seq_contig = exactkv.Engine(model, 2, LMAX + G).kv_bytes() - exactkv.Engine(model, 1, LMAX + G).kv_bytes()
+    torch.cuda.empty_cache()
+    rng = np.random.Generator(np.random.PCG64(7))
+    lens = rng.integers(1024, LMAX + 1, size=4096)
+    need = -(-(lens + G) // 16)
+    num_pages = int(budget * 0.97 // page_bytes)                     # ~3% for the raw pools and tails
+    n_fit = int(np.searchsorted(np.cumsum(need), num_pages, side="right"))
+    B = min(n_fit, 2048)
+    fit_contig = int(budget // per_seq_contig)
+    print(f"[e2e_paged] pool {num_pages} pages: {B} sequences (contiguous would fit {fit_contig})",
+          file=sys.stderr, flush=True)
+    eng = exactkv.PagedEngine(model, B, LMAX + G, backend="exactkv", num_pages=num_pages)
+    g = torch.Generator().manual_seed(1)
+    t0 = time.perf_counter()
+    toks = []
+    for i in range(B):
+        ids = torch.randint(0, cfg["vocab_size"], (int(lens[i]),), generator=g).to(dev)
+        toks.append(eng.add(ids)[1])
+        if i % 64 == 63:
+            print(f"[e2e_paged] prefilled {i + 1}", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    t = torch.stack(toks)
+    for s in range(G - 1):
+        t = eng.step(t).argmax(-1)
+        if s % 16 == 15:
+            print(f"[e2e_paged] step {s + 1}", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    tps = B * (G - 1) / (t2 - t1)
+    res = {
+        "metric": "paged e2e greedy decode tok/s, prompts U[1024, 4096] (Llama-3.1-8B random init)",
+        "value": round(tps, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random weights N(0,0.02), random token ids)",
+        "config": {"workload": "e2e_paged: mixed prompt lengths over one page pool", "gen": G,
+                   "prompt_lengths": "U[1024, 4096] seed 7", "pool_pages": num_pages,
+                   "kv_budget_gib": round(budget / 2**30, 2)},
+        "sequences": B, "contiguous_sequences_fit": fit_contig, "fit_ratio": round(B / max(fit_contig, 1), 3),
+        "mean_prompt": round(float(lens[:B].mean()), 1), "ms_per_step": round((t2 - t1) / (G - 1) * 1e3, 2),
+        "prefill_s": round(t1 - t0, 1), "pool_grows": eng.grows, "free_pages_after": eng.table.free_pages(),
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(res), flush=True)
 
 
 def e2e(a):

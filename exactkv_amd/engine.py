@@ -252,7 +252,9 @@ class PagedEngine:
     Engine's. Steps run eagerly: the block table and lengths change on the host between
     steps (begin_step claims a page whenever a token fills one)."""
 
-    def __init__(self, model, max_seqs, T_max, backend="exactkv", num_pages=None):
+    def __init__(self, model, max_seqs, T_max, backend="exactkv", num_pages=None, graph=True):
+        """graph: replay the step from a HIP graph when the step's slots are 0..n-1 (default);
+        the graph is captured again when n or a raw pool's buffer changes."""
         from .paged import PageTable, PagedBF16KV, PagedCompressedKV
         cfg = model.config
         self.m = model
@@ -272,6 +274,12 @@ class PagedEngine:
         self.rope = importlib.import_module(type(model.model.layers[0].self_attn).__module__).apply_rotary_pos_emb
         self.qk_norm = hasattr(model.model.layers[0].self_attn, "k_norm")
         self.grows = 0
+        self.use_graph = bool(graph)
+        self._stream = torch.cuda.Stream(device=self.dev) if self.use_graph else None
+        self._graph, self._graph_key, self._warm = None, None, set()
+        self._tok = torch.zeros(max_seqs, dtype=torch.long, device=self.dev)
+        self._logits = None
+        self.captures = 0
 
     @torch.no_grad()
     def add(self, ids, slot=None):
@@ -285,13 +293,9 @@ class PagedEngine:
     def release(self, slot):
         self.table.release(slot)
 
-    @torch.no_grad()
-    def step(self, tok, slots=None):
-        """tok: [n] the current token of each slot in `slots` (default: every live slot, in
-        order). Returns logits [n, vocab] for their next tokens."""
+    def _forward(self, tok, n):
+        """The step's kernels for n rows (appends, attention, the model): no host state."""
         m = self.m
-        slots = self.table.begin_step(slots)
-        n = len(slots)
         _, _, lens = self.table.step_rows()
         pos = (lens - 1).view(n, 1).long()                                   # each sequence's position
         h = m.model.embed_tokens(tok.view(n, 1))
@@ -300,14 +304,49 @@ class PagedEngine:
             att = layer.self_attn
             q, k, v = _project(self, att, layer.input_layernorm(h), n, cos, sin)
             kc, vc = self.kv[i]
-            kc.append(k[:, :, 0])
-            vc.append(v[:, 0])
+            kc._launch_append(k[:, :, 0])
+            vc._launch_append(v[:, 0])
             o = decode_attention(q[:, :, 0].contiguous(), kc, vc, window=self.windows[i])
             h = h + att.o_proj(o.reshape(n, 1, self.Hq * self.D))
             h = h + layer.mlp(layer.post_attention_layernorm(h))
-        if self.table.filled_in_step():
-            self.grows += check_overflow([c for kv in self.kv for c in kv])
         return m.lm_head(m.model.norm(h))[:, 0]
+
+    @torch.no_grad()
+    def step(self, tok, slots=None):
+        """tok: [n] the current token of each slot in `slots` (default: every live slot, in
+        order). Returns logits [n, vocab] for their next tokens."""
+        slots = self.table.begin_step(slots)
+        n = len(slots)
+        caches = [c for kv in self.kv for c in kv]
+        for c in caches:
+            c._check_append((n, self.Hkv, self.D))
+        dense = self.table.step_rows()[0] is None
+        if not (self.use_graph and dense):
+            logits = self._forward(tok, n)
+        else:
+            cur = torch.cuda.current_stream(self.dev)
+            self._stream.wait_stream(cur)
+            with torch.cuda.stream(self._stream):
+                self._tok[:n].copy_(tok)
+                key = (n, tuple(c.raw.data_ptr() for c in caches if hasattr(c, "raw")))
+                if n not in self._warm:                  # first step at this n: eager, on the graph's stream
+                    logits = self._forward(self._tok[:n], n)
+                    self._warm.add(n)
+                else:
+                    if self._graph is None or key != self._graph_key:
+                        self._graph = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(self._graph, stream=self._stream):
+                            self._logits = self._forward(self._tok[:n], n)
+                        self._graph_key = key
+                        self.captures += 1
+                    self._graph.replay()
+                    logits = self._logits.clone()
+            cur.wait_stream(self._stream)
+        for c in caches:
+            c._advance()
+        if self.table.filled_in_step():
+            self.grows += check_overflow(caches)
+        return logits
 
     def kv_bytes(self):
         return sum(c.nbytes() for kv in self.kv for c in kv)

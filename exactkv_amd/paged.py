@@ -247,18 +247,27 @@ class PagedCompressedKV:
 
     def append(self, x):
         """x: [n, H, D] bf16, row i the new token of the current step's slot i (begin_step)."""
+        self._check_append(tuple(x.shape))
+        self._launch_append(x)
+        self._advance()
+
+    # append in three parts, so that a captured step can replay the kernels alone
+    def _check_append(self, shape):
         t = self.table
         if self._appended == t.step:
             raise RuntimeError("append called twice in one table step (call table.begin_step first)")
         if self._pending is not None:
             raise RuntimeError("call check_overflow() after a step that filled pages before appending again")
-        slots, _, _ = t.step_rows()
-        if x.shape != (len(t._step_slots), self.H, self.D):
+        t.step_rows()
+        if shape != (len(t._step_slots), self.H, self.D):
             raise ValueError(f"append expects [{len(t._step_slots)}, {self.H}, {self.D}] (one row per step slot)")
-        append_paged(x, self._buf(), t, slots)
-        self._appended = t.step
-        filled = t.filled_in_step()
-        self._pending = filled or None
+
+    def _launch_append(self, x):
+        append_paged(x, self._buf(), self.table, self.table.step_rows()[0])
+
+    def _advance(self):
+        self._appended = self.table.step
+        self._pending = self.table.filled_in_step() or None
 
     def finish_page(self, overflowed, cnt=None):
         """check_overflow's per-cache step: re-encode the pages of the last append if the raw pool
@@ -335,14 +344,23 @@ class PagedBF16KV:
         self.prefill(slot, x)
 
     def append(self, x):
+        self._check_append(tuple(x.shape))
+        self._launch_append(x)
+        self._advance()
+
+    def _check_append(self, shape):
         t = self.table
         if self._appended == t.step:
             raise RuntimeError("append called twice in one table step (call table.begin_step first)")
-        slots, _, _ = t.step_rows()
-        if x.shape != (len(t._step_slots), self.H, self.D):
+        t.step_rows()
+        if shape != (len(t._step_slots), self.H, self.D):
             raise ValueError(f"append expects [{len(t._step_slots)}, {self.H}, {self.D}] (one row per step slot)")
-        append_paged_bf16(x, self.buf, t, slots)
-        self._appended = t.step
+
+    def _launch_append(self, x):
+        append_paged_bf16(x, self.buf, self.table, self.table.step_rows()[0])
+
+    def _advance(self):
+        self._appended = self.table.step
 
     def nbytes(self):
         return self.buf.numel() * 2

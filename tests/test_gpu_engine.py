@@ -245,3 +245,27 @@ def test_paged_engine_ragged_sequences_join_and_leave():
             err = (have - want).abs().max().item()
             assert err <= 0.03 * want.abs().max().item(), (sl, err)
     assert ec.table.free_pages() < ec.table.num_pages
+
+
+def test_paged_engine_graph_replay_and_growth():
+    """The paged engine's HIP-graph steps equal its eager steps bit for bit, also across a
+    raw-pool growth between steps (which makes it capture the step again)."""
+    import exactkv_amd as exactkv
+    m = _model("llama")
+    ids = _ids(seed=17)
+    eg = exactkv.PagedEngine(m, B, PROMPT + NEW, backend="exactkv", graph=True)
+    ee = exactkv.PagedEngine(m, B, PROMPT + NEW, backend="exactkv", graph=False)
+    tg = torch.stack([eg.add(ids[b])[1] for b in range(B)])
+    te = torch.stack([ee.add(ids[b])[1] for b in range(B)])
+    assert torch.equal(tg, te)
+    print("[engine] paged graph vs eager", flush=True)
+    for s in range(NEW - 1):
+        if s == 9:
+            c = eg.kv[1][0]
+            cap = c.cap
+            c._grow(c.cap + 1)
+            assert c.cap > cap
+        lg, le = eg.step(tg), ee.step(te)
+        assert torch.equal(lg.view(torch.int16), le.view(torch.int16)), s
+        tg, te = lg.argmax(-1), le.argmax(-1)
+    assert eg.captures >= 2 and ee.captures == 0

@@ -214,7 +214,7 @@ def main():
         a.copies = 1
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
-              "(the decode path shards by KV head or sequence with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the decode path shards by KV head or sequence with no exchange)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -5,8 +5,9 @@
 //   1. enc_pages_kernel  one wavefront per (sequence, page, head): exponent window,
 //                        zero flag, codes, sign|mantissa bytes, base bytes, rowmask
 //                        (reference kernels.py:216-264, codec.py:31-49);
-//   2. scan_kernel       one workgroup: rowoff = counter + exclusive running count of raw
-//                        rows over the call's pages in (sequence, page, head) order; the
+//   2. the slot scan     rowoff = counter + exclusive running count of raw rows over the
+//                        call's pages in (sequence, page, head) order, in three launches
+//                        (block counts, a scan of the block totals, the writes); the
 //                        counter advances by the total (codec.py:50-53 order; the
 //                        reference GPU encoder used an atomic counter, kernels.py:262);
 //   3. rawcopy_kernel    copies raw rows into their slots, skipping slots >= cap
@@ -120,30 +121,130 @@ __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunit
                 a.rowmask + page);
 }
 
-__global__ void __launch_bounds__(1024) scan_kernel(EncArgs a, int64_t nunits) {
-    const int64_t per = (nunits + 1023) / 1024;
-    const int64_t u0 = threadIdx.x * per;
-    const int64_t u1 = min(u0 + per, nunits);
+// Units u0 .. u1-1 of one scan thread, walked in order: coordinates by increment (one
+// division per thread), page indices and masks 8 at a time with every load of a group
+// issued before the first is used (clamped, no branch).
+struct UnitWalk {
+    int bi, pg, hk;
+    __device__ void next(const EncArgs& a) {
+        if (++hk == a.H) {
+            hk = 0;
+            if (++pg == a.npg) {
+                pg = 0;
+                ++bi;
+            }
+        }
+    }
+};
+
+__device__ inline void unit_group8(const EncArgs& a, UnitWalk& w, int64_t c, int64_t u1, int64_t page[8],
+                                   int n[8]) {
+    int bi[8], pg[8], hk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        bi[k] = w.bi;
+        pg[k] = w.pg;
+        hk[k] = w.hk;
+        if (c + k + 1 < u1) w.next(a);                 // stays on the last unit past the end
+    }
+    if (a.dst_pages == nullptr) {                      // uniform
+#pragma unroll
+        for (int k = 0; k < 8; ++k) page[k] = ((int64_t)(a.b0 + bi[k]) * (a.TS / kPage) + (a.pg0 + pg[k])) * a.H + hk[k];
+    } else {
+        int32_t e[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = a.dst_pages[bi[k] * a.dst_stride + pg[k]];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            page[k] = (int64_t)min((uint64_t)(uint32_t)e[k], (uint64_t)(a.all_pages - 1)) * a.H + hk[k];
+    }
+    uint32_t m[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = (uint32_t)a.rowmask[page[k]];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) n[k] = c + k < u1 ? popc32(m[k]) : 0;
+}
+
+// The slot scan in three launches over blocks of kScanUnits units (1024 threads x 8):
+//   scan_count_kernel   block g: its units' raw rows -> the rowoff slot of its first unit;
+//   scan_blocks_kernel  one workgroup: exclusive scan of the block totals from the
+//                       counter -> the same slots; the counter advances by the total;
+//   scan_write_kernel   block g: rowoff = its slot's offset + running count in unit order.
+// The block totals need no workspace: the slot of a block's first unit is rewritten last.
+constexpr int64_t kScanUnits = 1024 * 8;
+
+__device__ inline int64_t first_page_of(const EncArgs& a, int64_t g) {
+    int bi, pg, hk;
+    unit_coords(a, g * kScanUnits, bi, pg, hk);
+    return unit_page(a, bi, pg, hk);
+}
+
+__device__ inline int block_units(const EncArgs& a, int64_t nunits, int64_t& u0, int64_t& u1, int64_t page[8],
+                                  int n[8]) {
+    const int64_t b0 = (int64_t)blockIdx.x * kScanUnits;
+    u0 = min(b0 + (int64_t)threadIdx.x * 8, nunits);
+    u1 = min(u0 + 8, nunits);
+    int local = 0;
+    if (u0 < u1) {
+        UnitWalk w{0, 0, 0};
+        unit_coords(a, u0, w.bi, w.pg, w.hk);
+        unit_group8(a, w, u0, u1, page, n);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) local += n[k];
+    }
+    return local;
+}
+
+__global__ void __launch_bounds__(1024) scan_count_kernel(EncArgs a, int64_t nunits) {
+    int64_t u0, u1, page[8];
+    int n[8];
+    const int local = block_units(a, nunits, u0, u1, page, n);
+    int total;
+    block_excl_scan(local, total);
+    if (threadIdx.x == 0) a.rowoff[first_page_of(a, blockIdx.x)] = total;
+}
+
+__global__ void __launch_bounds__(1024) scan_blocks_kernel(EncArgs a, int64_t nblocks) {
+    const int64_t per = (nblocks + 1023) / 1024;
+    const int64_t g0 = min((int64_t)threadIdx.x * per, nblocks), g1 = min(g0 + per, nblocks);
     const int cnt0 = *a.cnt;
     int local = 0;
-    for (int64_t u = u0; u < u1; ++u) {
-        int bi, pg, hk;
-        unit_coords(a, u, bi, pg, hk);
-        local += popc32((uint32_t)a.rowmask[unit_page(a, bi, pg, hk)]);
-    }
+    for (int64_t g = g0; g < g1; ++g) local += a.rowoff[first_page_of(a, g)];
     int total;
     int run = cnt0 + block_excl_scan(local, total);
-    for (int64_t u = u0; u < u1; ++u) {
-        int bi, pg, hk;
-        unit_coords(a, u, bi, pg, hk);
-        const int64_t page = unit_page(a, bi, pg, hk);
-        a.rowoff[page] = run;
-        run += popc32((uint32_t)a.rowmask[page]);
+    for (int64_t g = g0; g < g1; ++g) {
+        const int64_t p = first_page_of(a, g);
+        const int t = a.rowoff[p];
+        a.rowoff[p] = run;
+        run += t;
     }
     if (threadIdx.x == 0) {
         if (a.before) *a.before = cnt0;
         *a.cnt = cnt0 + total;
     }
+}
+
+__global__ void __launch_bounds__(1024) scan_write_kernel(EncArgs a, int64_t nunits) {
+    __shared__ int s_base;
+    if (threadIdx.x == 0) s_base = a.rowoff[first_page_of(a, blockIdx.x)];
+    __syncthreads();                                   // read before the slot is rewritten
+    int64_t u0, u1, page[8];
+    int n[8];
+    const int local = block_units(a, nunits, u0, u1, page, n);
+    int total;
+    int run = s_base + block_excl_scan(local, total);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if (u0 + k < u1) a.rowoff[page[k]] = run;
+        run += n[k];
+    }
+}
+
+static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
+    const int64_t nb = (n + kScanUnits - 1) / kScanUnits;
+    hipLaunchKernelGGL(scan_count_kernel, dim3((unsigned)nb), dim3(1024), 0, stream, a, n);
+    hipLaunchKernelGGL(scan_blocks_kernel, dim3(1), dim3(1024), 0, stream, a, nb);
+    hipLaunchKernelGGL(scan_write_kernel, dim3((unsigned)nb), dim3(1024), 0, stream, a, n);
 }
 
 // Copy one page's raw rows (token p's row at src + p*s_p) into slots rowoff + k (< cap).
@@ -467,7 +568,7 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
     const unsigned grid = (unsigned)((n + 3) / 4);
     hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, a, n);
+    launch_scan(a, n, stream);
     hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     return launch_status("encode_pages");
 }
@@ -498,7 +599,7 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     a.all_pages = (int64_t)B * (TS / kPage);
     const unsigned grid = (unsigned)((n + 3) / 4);
     hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, a, n);
+    launch_scan(a, n, stream);
     hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     return launch_status("encode_pages_paged");
 }

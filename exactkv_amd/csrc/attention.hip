@@ -604,6 +604,9 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         uint4 v = lds16(lds_ptr(qst + (uint32_t)(r * 256 + 2 * d0)));
         if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
         qop[kc] = as_bf16x8(v.x, v.y, v.z, v.w);
+        // pin the masked operand: left alone, the compiler re-applies the mask (16 selects)
+        // before every page's score MFMAs instead of keeping the result
+        asm volatile("" : "+v"(qop[kc]));
     }
     if constexpr (COMP) {
         vmk = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 4u * lane));

@@ -93,9 +93,20 @@ def call(name, *args):
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
 
 
-def stream():
+_raw_stream = None
+
+
+def stream(index=None):
+    """The current HIP stream of device `index` (default: the current device) as an integer,
+    through torch's raw-stream query when it has one (a few µs cheaper per call than
+    building a torch Stream object)."""
+    global _raw_stream
     import torch
-    return torch.cuda.current_stream().cuda_stream
+    if _raw_stream is None:
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+    if _raw_stream:
+        return _raw_stream(torch.cuda.current_device() if index is None else index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def ptr(t, align=16, what="tensor"):

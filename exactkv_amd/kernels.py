@@ -49,8 +49,8 @@ _WS = {}  # split partials, reused per (device, stream, rows, nsplit): kernels o
 _CNT = {}  # merge arrival counters per (device, stream, units): zero between calls
 
 
-def _workspace(dev, rows, ns):
-    key = (dev.index, _lib.stream(), rows, ns)
+def _workspace(dev, rows, ns, st=None):
+    key = (dev.index, _lib.stream(dev.index) if st is None else st, rows, ns)
     ws = _WS.get(key)
     if ws is None:
         f32 = dict(device=dev, dtype=torch.float32)
@@ -174,17 +174,18 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     window = _window_arg(window)
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
-    wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    st = _lib.stream(q.device.index)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns, st)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     if block_table is not None:
         _lib.call("exkv_attn_compressed_paged", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
                   cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B, Hq, Hkv, D,
-                  int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream())
+                  int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, st)
         return out
     _lib.call("exkv_attn_compressed", _lib.ptr(q), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
               cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E,
-              _lib.stream())
+              st)
     return out
 
 
@@ -208,17 +209,18 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     window = _window_arg(window)
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
-    wo, wm, wl = _workspace(q.device, B * Hq, ns)
+    st = _lib.stream(q.device.index)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns, st)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     if block_table is not None:
         _lib.call("exkv_attn_bf16_paged", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
                   wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), bt, bts, pool_pages, B,
-                  Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream())
+                  Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window, D ** -0.5 * LOG2E, st)
         return out
     _lib.call("exkv_attn_bf16", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), wo.data_ptr(), wm.data_ptr(),
               wl.data_ptr(), cnt.data_ptr() if cnt is not None else None, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp, lstride, ns, sl, window,
-              D ** -0.5 * LOG2E, _lib.stream())
+              D ** -0.5 * LOG2E, st)
     return out
 
 

@@ -101,8 +101,11 @@ def _cache_args(c):
         raw = c["raw"]
         args = (c["sm"], c["code"], c["base"], c["rowmask"], c["rowoff"], raw)
     else:
-        B, TS, H = c.B, c.TS, c.H
         args = c.kernel_args()
+        memo = getattr(c, "_abi_memo", None)
+        if memo is not None and memo[0] is args:      # the same buffers as last call
+            return memo[1]
+        B, TS, H = c.B, c.TS, c.H
         raw = args[5]
     for t, name in zip(args, ("sm", "code", "base", "rowmask", "rowoff", "raw")):
         if not t.is_contiguous():
@@ -110,7 +113,10 @@ def _cache_args(c):
     if raw.shape[0] < 1:
         raise ValueError("raw pool must have at least one row")
     ptrs = [_lib.ptr(t, what=n) for t, n in zip(args, ("sm", "code", "base", "rowmask", "rowoff", "raw"))]
-    return (*ptrs, raw.shape[0]), TS, H, B
+    res = (*ptrs, raw.shape[0]), TS, H, B
+    if not isinstance(c, dict):
+        c._abi_memo = (args, res)                      # kernel_args() is rebuilt when the pool grows
+    return res
 
 
 def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window=0):

@@ -26,6 +26,7 @@ SIGNATURES = {
                                 _i32, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_bf16_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_decode_to_bf16_paged": [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _p],
     "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
                              _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_attn_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32,

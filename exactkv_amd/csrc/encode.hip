@@ -516,6 +516,10 @@ struct DecArgs {
     CSrc c;
     uint16_t* out;            // [B, T, H, 128]
     int B, T, TS, H;
+    // paged: page pg of sequence b is pool page bt[b * bt_stride + pg] (clamped to pool_pages)
+    const int32_t* bt = nullptr;
+    int64_t bt_stride = 0;
+    int64_t pool_pages = 0;
 };
 
 // One wavefront per (sequence, page, head), through the attention kernels' page decoder.
@@ -529,8 +533,10 @@ __global__ void __launch_bounds__(256) decode_kernel(DecArgs a) {
     const int b = (int)(u / ((int64_t)a.H * NP));
     if (pg * kPage >= a.T) return;
     const int t = pg * kPage + r;
+    const int64_t pidx = a.bt ? (int64_t)min((uint32_t)a.bt[b * a.bt_stride + pg], (uint32_t)(a.pool_pages - 1))
+                              : (int64_t)b * NP + pg;
     PageBytes pb;
-    load_page(a.c, ((int64_t)b * a.TS + t) * a.H + h, ((int64_t)b * NP + pg) * a.H + h, g, pb);
+    load_page(a.c, (pidx * kPage + r) * a.H + h, pidx * a.H + h, g, pb);
     uint32_t v[16];
     rebuild_page(a.c, pb, r, g, v);
     if (t >= a.T) return;
@@ -682,6 +688,31 @@ extern "C" int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h,
     hipLaunchKernelGGL(paged_bf16_append_kernel, dim3((unsigned)((n * H + 3) / 4)), dim3(256), 0, stream, a,
                        (uint16_t*)buf);
     return launch_status("bf16_append_paged");
+}
+
+extern "C" int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base,
+                                         const int32_t* rowmask, const int32_t* rowoff, const void* raw,
+                                         int64_t raw_rows, int64_t pool_pages, const int32_t* block_table,
+                                         int64_t bt_stride, void* out, int32_t B, int32_t T, int32_t H, int32_t D,
+                                         hipStream_t stream) {
+    EXKV_REQUIRE(D == kD, "decode_to_bf16_paged: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(B > 0 && H > 0 && bt_stride > 0 && pool_pages > 0, "decode_to_bf16_paged: bad shape");
+    EXKV_REQUIRE(T >= 0 && T <= bt_stride * kPage, "decode_to_bf16_paged: T=%d exceeds the table's %lld pages", T,
+                 (long long)bt_stride);
+    EXKV_REQUIRE(raw_rows > 0, "decode_to_bf16_paged: empty raw pool");
+    EXKV_REQUIRE(sm && code && base && rowmask && rowoff && raw && out && block_table,
+                 "decode_to_bf16_paged: null pointer");
+    if (T == 0) return EXKV_OK;
+    const int TS = (T + kPage - 1) / kPage * kPage;     // pages the tokens touch
+    DecArgs a{CSrc{(const uint8_t*)sm, (const uint8_t*)code, (const uint8_t*)base, rowmask, rowoff,
+                   (const uint16_t*)raw, raw_rows},
+              (uint16_t*)out, B, T, TS, H};
+    a.bt = block_table;
+    a.bt_stride = bt_stride;
+    a.pool_pages = pool_pages;
+    const int64_t n = (int64_t)B * (TS / kPage) * H;
+    hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a);
+    return launch_status("decode_to_bf16_paged");
 }
 
 extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,

@@ -230,11 +230,19 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     return out
 
 
-def decode_to_bf16(c, T):
+def decode_to_bf16(c, T, block_table=None):
     """Compressed buffers (a buffers() dict or CompressedKV) -> bf16 [B, T, H, 128],
-    through the same page decoder attention uses."""
+    through the same page decoder attention uses. block_table (int32 [B, max_pages] on the
+    GPU): c is a pool of pages and sequence b's page p is pool page block_table[b, p]."""
     ka, TS, H, B = _cache_args(c)
     dev = (c["sm"] if isinstance(c, dict) else c.sm).device
+    if block_table is not None:
+        bt, bts, cap = _block_table_arg(block_table, block_table.shape[0])
+        Bq = block_table.shape[0]
+        out = torch.empty(Bq, T, H, D_SUPPORTED, dtype=torch.bfloat16, device=dev)
+        _lib.call("exkv_decode_to_bf16_paged", *ka, B * TS // P, bt, bts, _lib.ptr(out), Bq, int(T), H,
+                  D_SUPPORTED, _lib.stream(dev.index))
+        return out
     out = torch.empty(B, T, H, D_SUPPORTED, dtype=torch.bfloat16, device=dev)
     _lib.call("exkv_decode_to_bf16", *ka, _lib.ptr(out), B, int(T), TS, H, D_SUPPORTED, _lib.stream())
     return out

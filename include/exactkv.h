@@ -153,6 +153,15 @@ int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, cons
                         const int32_t* rowoff, const void* raw, int64_t raw_rows, void* out, int32_t B,
                         int32_t T, int32_t TS, int32_t H, int32_t D, hipStream_t stream);
 
+/* decode_to_bf16 over a paged cache (arrays of pool_pages pages): out [B, T, H, 128] holds
+ * tokens [0, T) of each sequence b, page p read from pool page block_table[b*bt_stride + p]
+ * (entries clamped to the pool; T <= 16*bt_stride). No counterpart in the reference
+ * (contiguous caches only; paged KV is in its future work, README.md:121-123). */
+int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base, const int32_t* rowmask,
+                              const int32_t* rowoff, const void* raw, int64_t raw_rows, int64_t pool_pages,
+                              const int32_t* block_table, int64_t bt_stride, void* out, int32_t B, int32_t T,
+                              int32_t H, int32_t D, hipStream_t stream);
+
 /* Split-K GQA decode attention over compressed K and V caches, then the split merge.
  * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
  * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: B*(Hkv/gcd(Hkv,8))*ceil(Hq/Hkv/16) i32 arrival

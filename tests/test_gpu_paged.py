@@ -171,7 +171,18 @@ def test_paged_cache_prefill_append_release_compact():
         exactkv.check_overflow([kc, vc])
 
     def check_contents():
+        live = table.live_slots()
         for c, b in ((kc, kb), (vc, vb)):
+            # through the block table: each live slot's tokens in order
+            Tm = max(table.length(s) for s in live)
+            if Tm:
+                bt = table.block_table.index_select(0, torch.tensor(live, device=DEV))
+                dec_bt = kernels.decode_to_bf16(c.buffers(), Tm, block_table=bt)
+                for i, s in enumerate(live):
+                    T = table.length(s)
+                    if T:
+                        want = torch.stack(truth[s][0 if c is kc else 1]).to(DEV)
+                        assert same_bits(dec_bt[i, :T], want), f"slot {s} (block table)"
             dec = kernels.decode_to_bf16(c.buffers(), c.TS)
             for s in table.live_slots():
                 pages, T = table.pages(s), table.length(s)

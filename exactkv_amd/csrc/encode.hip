@@ -21,52 +21,85 @@ namespace exkv {
 
 __device__ inline uint8_t sm_byte(uint32_t u) { return (uint8_t)(((u >> 8) & 0x80u) | (u & 0x7Fu)); }
 
-// Encode one 16-token page of one head. Lane l owns channels l and l + 64, so a code
-// byte (channel j low nibble, j + 64 high nibble) is produced by one lane. Token p's
-// source row is src + p * s_p, except row 15 which comes from `last` when given.
-// Destination rows of consecutive tokens are `rs` rows apart (rs = H).
+// Encode one 16-token page of one head. Lane l = (half, m): tokens 8*half .. 8*half+7,
+// channels 2m, 2m+1, 2m+64 and 2m+65 -- so each code byte (channel j low nibble, j + 64
+// high nibble) and each pair of sm / code bytes is produced by one lane, and every load and
+// store moves two channels (half the instructions of one channel per lane). The two halves
+// combine their per-channel maxima with one cross-half shuffle. Token p's source row is
+// src + p * s_p, except row 15 which comes from `last` when given; rows must be 4-byte
+// aligned (even element offsets: callers check). Destination rows of consecutive tokens
+// are `rs` rows apart (rs = H).
 __device__ void encode_page(const uint16_t* src, int64_t s_p, const uint16_t* last, int lane,
                             uint8_t* sm0, uint8_t* code0, int64_t rs, uint8_t* basep, int32_t* rmaskp) {
-    uint32_t ulo[kPage], uhi[kPage];
+    const int half = lane >> 5, m = lane & 31;
+    uint32_t lo[8], hi[8];                             // bf16 pairs: channels (2m, 2m+1), (2m+64, 2m+65)
 #pragma unroll
-    for (int p = 0; p < kPage; ++p) {
+    for (int i = 0; i < 8; ++i) {
+        const int p = 8 * half + i;
         const uint16_t* rp = (p == kPage - 1 && last != nullptr) ? last : src + p * s_p;
-        ulo[p] = rp[lane];
-        uhi[p] = rp[lane + 64];
+        lo[i] = *reinterpret_cast<const uint32_t*>(rp + 2 * m);
+        hi[i] = *reinterpret_cast<const uint32_t*>(rp + 64 + 2 * m);
     }
-    int top_lo = 0, top_hi = 0;
-    bool z_lo = false, z_hi = false;
+    // per channel c (0: 2m, 1: 2m+1, 2: 2m+64, 3: 2m+65): exponent window over 16 tokens
+    auto ex = [&](int i, int c) -> int {
+        const uint32_t w = c < 2 ? lo[i] : hi[i];
+        return (int)((w >> (c & 1 ? 23 : 7)) & 255u);
+    };
+    int top[4] = {0, 0, 0, 0}, zer[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int p = 0; p < kPage; ++p) {
-        const int el = (ulo[p] >> 7) & 255, eh = (uhi[p] >> 7) & 255;
-        top_lo = max(top_lo, el);
-        top_hi = max(top_hi, eh);
-        z_lo |= el == 0;
-        z_hi |= eh == 0;
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = ex(i, c);
+            top[c] = max(top[c], e);
+            zer[c] |= e == 0;
+        }
+    int fl[4];
+    bool zf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        top[c] = max(top[c], __shfl_xor(top[c], 32));
+        zer[c] |= __shfl_xor(zer[c], 32);
+        fl[c] = max(top[c] - 15, 0);
+        zf[c] = zer[c] && fl[c] > 0;
     }
-    const int fl_lo = max(top_lo - 15, 0), fl_hi = max(top_hi - 15, 0);
-    const bool zf_lo = z_lo && fl_lo > 0, zf_hi = z_hi && fl_hi > 0;
     uint32_t esc = 0;
 #pragma unroll
-    for (int p = 0; p < kPage; ++p) {
-        const int el = (ulo[p] >> 7) & 255, eh = (uhi[p] >> 7) & 255;
-        const int cl = (zf_lo && el == 0) ? 0 : el - fl_lo;
-        const int ch = (zf_hi && eh == 0) ? 0 : eh - fl_hi;
-        const bool ok_lo = fl_lo < 128 && cl >= ((zf_lo && el != 0) ? 1 : 0);
-        const bool ok_hi = fl_hi < 128 && ch >= ((zf_hi && eh != 0) ? 1 : 0);
-        esc |= (uint32_t)!(ok_lo && ok_hi) << p;
+    for (int i = 0; i < 8; ++i) {
+        const int p = 8 * half + i;
+        int nib[4];
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = ex(i, c);
+            const int cd = (zf[c] && e == 0) ? 0 : e - fl[c];
+            ok = ok && fl[c] < 128 && cd >= ((zf[c] && e != 0) ? 1 : 0);
+            nib[c] = min(max(cd, 0), 15);
+        }
+        esc |= (uint32_t)!ok << i;
+        // sm bytes of the two pairs, and the code bytes 2m (nib 0 | nib 2 << 4), 2m+1 (1 | 3)
+        const uint32_t smlo = ((lo[i] >> 8) & 0x80u) | (lo[i] & 0x7Fu) | (((lo[i] >> 24) & 0x80u) | ((lo[i] >> 16) & 0x7Fu)) << 8;
+        const uint32_t smhi = ((hi[i] >> 8) & 0x80u) | (hi[i] & 0x7Fu) | (((hi[i] >> 24) & 0x80u) | ((hi[i] >> 16) & 0x7Fu)) << 8;
         uint8_t* sp = sm0 + p * rs * 128;
-        sp[lane] = sm_byte(ulo[p]);
-        sp[lane + 64] = sm_byte(uhi[p]);
-        const int nl = min(max(cl, 0), 15), nh = min(max(ch, 0), 15);
-        code0[p * rs * 64 + lane] = (uint8_t)(nl | (nh << 4));
+        *reinterpret_cast<uint16_t*>(sp + 2 * m) = (uint16_t)smlo;
+        *reinterpret_cast<uint16_t*>(sp + 64 + 2 * m) = (uint16_t)smhi;
+        *reinterpret_cast<uint16_t*>(code0 + p * rs * 64 + 2 * m) =
+            (uint16_t)((nib[0] | (nib[2] << 4)) | ((nib[1] | (nib[3] << 4)) << 8));
     }
-    basep[lane] = (uint8_t)min(fl_lo + (zf_lo ? 128 : 0), 255);
-    basep[lane + 64] = (uint8_t)min(fl_hi + (zf_hi ? 128 : 0), 255);
+    if (half == 0) {
+        const uint32_t b0 = (uint32_t)min(fl[0] + (zf[0] ? 128 : 0), 255), b1 = (uint32_t)min(fl[1] + (zf[1] ? 128 : 0), 255);
+        const uint32_t b2 = (uint32_t)min(fl[2] + (zf[2] ? 128 : 0), 255), b3 = (uint32_t)min(fl[3] + (zf[3] ? 128 : 0), 255);
+        *reinterpret_cast<uint16_t*>(basep + 2 * m) = (uint16_t)(b0 | (b1 << 8));
+        *reinterpret_cast<uint16_t*>(basep + 64 + 2 * m) = (uint16_t)(b2 | (b3 << 8));
+    }
+    // rowmask: ballot bit l < 32 is token i (half 0), bit 32 + l token 8 + i
     uint32_t rm = 0;
 #pragma unroll
-    for (int p = 0; p < kPage; ++p)
-        if (__ballot((esc >> p) & 1u) != 0) rm |= 1u << p;
+    for (int i = 0; i < 8; ++i) {
+        const uint64_t bal = __ballot((esc >> i) & 1u);
+        if ((uint32_t)bal != 0u) rm |= 1u << i;
+        if ((uint32_t)(bal >> 32) != 0u) rm |= 1u << (8 + i);
+    }
     if (lane == 0) *rmaskp = (int32_t)rm;
 }
 
@@ -568,6 +601,8 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
     EXKV_REQUIRE(cap >= 0 && cap <= raw_rows, "encode_pages: cap %lld exceeds the raw pool (%lld rows)",
                  (long long)cap, (long long)raw_rows);
     EXKV_REQUIRE(src && sm && code && base && rowmask && rowoff && raw && cnt, "encode_pages: null pointer");
+    EXKV_REQUIRE((uintptr_t)src % 4 == 0 && s_b % 2 == 0 && s_pg % 2 == 0 && s_p % 2 == 0 && s_h % 2 == 0,
+                 "encode_pages: source rows must start at even elements (4-byte aligned)");
     const int64_t n = (int64_t)nb * npg * H;
     if (n == 0) return EXKV_OK;
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
@@ -596,6 +631,8 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     EXKV_REQUIRE(cap >= 0 && cap <= raw_rows, "encode_pages_paged: cap %lld exceeds the raw pool (%lld rows)",
                  (long long)cap, (long long)raw_rows);
     EXKV_REQUIRE(src && sm && code && base && rowmask && rowoff && raw && cnt, "encode_pages_paged: null pointer");
+    EXKV_REQUIRE((uintptr_t)src % 4 == 0 && s_b % 2 == 0 && s_pg % 2 == 0 && s_p % 2 == 0 && s_h % 2 == 0,
+                 "encode_pages_paged: source rows must start at even elements (4-byte aligned)");
     const int64_t n = (int64_t)nb * npg * H;
     if (n == 0) return EXKV_OK;
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
@@ -620,6 +657,8 @@ extern "C" int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void
                  "append: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
     EXKV_REQUIRE(x && sm && code && base && rowmask && rowoff && raw && cnt && before && state,
                  "append: null pointer");
+    EXKV_REQUIRE((uintptr_t)x % 4 == 0 && sx_b % 2 == 0 && sx_h % 2 == 0,
+                 "append: token rows must start at even elements (4-byte aligned)");
     AppendArgs a{(const uint16_t*)x, sx_b, sx_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base, rowmask, rowoff,
                  (uint16_t*)raw, cnt, before, state, cap, B, H, TS};
     const unsigned grid = (unsigned)((B * H + 3) / 4);
@@ -663,6 +702,8 @@ extern "C" int exkv_cache_append_paged(const void* x, int64_t sx_b, int64_t sx_h
                  "append_paged: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
     EXKV_REQUIRE(x && sm && code && base && rowmask && rowoff && raw && cnt && before && lens && block_table,
                  "append_paged: null pointer");
+    EXKV_REQUIRE((uintptr_t)x % 4 == 0 && sx_b % 2 == 0 && sx_h % 2 == 0,
+                 "append_paged: token rows must start at even elements (4-byte aligned)");
     if (n == 0) return EXKV_OK;
     PagedAppendArgs a{(const uint16_t*)x, sx_b, sx_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base, rowmask,
                       rowoff, (uint16_t*)raw, cnt, before, slots, lens, block_table, bt_stride, cap, n, H,

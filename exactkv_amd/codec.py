@@ -73,6 +73,19 @@ def decode_reference(c):
     return out.to(src) if src != dev else out
 
 
+_STORED = ("sm", "code", "base", "rowmask", "rowoff", "raw")
+
+
 def bits_per_value(c):
-    n = c["sm"].numel()
-    return sum(c[k].numel() * c[k].element_size() for k in ("sm", "code", "base", "rowmask", "rowoff", "raw")) * 8 / n
+    """Storage cost of an encoded tensor (reference codec.py:76-78): every allocated byte of
+    the six arrays, raw pool included, in bits per value of the [B, T, H, D] input. With N
+    raw rows that is 8 * (192 + 128/16 + 8/16 + 256 N / (B T H)) / 128 = 12.53125 +
+    16 N / (B T H) for D = 128."""
+    values = 1
+    for n in c["sm"].shape:
+        values *= n
+    total = 0
+    for name in _STORED:
+        t = c[name]
+        total += t.numel() * t.element_size()
+    return 8.0 * total / values

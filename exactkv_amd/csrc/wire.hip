@@ -157,6 +157,10 @@ __global__ void __launch_bounds__(1024) wire_scan_kernel(WireArgs a) {
     }
     int total;
     int run = start + block_excl_scan(local, total);
+    // unpack: the blob's rows must be exactly those its header declares -- the later blobs'
+    // pool slots and the counter are placed by the declared counts -- else skip it
+    int declared = total;
+    if (UNPACK && q.T >= 0) declared = (int)reinterpret_cast<const uint32_t*>(q.blob)[7];
     if (per <= kScanPer) {
 #pragma unroll
         for (int k = 0; k < kScanPer; ++k) {
@@ -170,9 +174,9 @@ __global__ void __launch_bounds__(1024) wire_scan_kernel(WireArgs a) {
         }
     }
     if (threadIdx.x == 0) {
-        ws[0] = q.T;
+        ws[0] = declared == total ? q.T : -1;
         ws[1] = start;
-        ws[2] = total;
+        ws[2] = declared;
     }
 }
 

@@ -135,6 +135,12 @@ def _check_blob(blob, cache):
         raise ValueError("inconsistent wire header")
     if blob.numel() < h["total"]:
         raise ValueError(f"blob of {blob.numel()} bytes is shorter than its header's {h['total']}")
+    npf = h["full_pages"] * cache.H
+    if npf:
+        rm = blob[h["off_rowmask"]: h["off_rowmask"] + 4 * npf].view(torch.int32)
+        rows = int(_popc16(rm & 0xFFFF).sum().item())
+        if rows != N:
+            raise ValueError(f"blob's rowmask marks {rows} raw rows, its header declares {N}")
     return h
 
 

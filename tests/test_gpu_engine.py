@@ -143,6 +143,53 @@ def test_fused_prefill_writes_the_same_cache(kind):
         assert torch.equal(va.buf.view(torch.int16), vf.buf.view(torch.int16))
 
 
+@pytest.mark.parametrize("kind", ["llama", "qwen3"])
+def test_write_through_prefill_equals_the_oracle_codec(kind):
+    """The write-through prefill's bytes against the oracle: the reference prefills with a
+    DynamicCache and copies each layer's K/V into its cache (engine.py:42-49,
+    cache.py:87-98), i.e. codec.encode of those tensors for the full pages and bf16 rows in
+    the tail area for the open page. Encode the model's own DynamicCache K/V with the CPU
+    oracle and compare every byte of every layer's caches."""
+    import numpy as np
+    import exactkv_amd as exactkv
+    from exactkv_amd.engine import _fused_sdpa
+    from oracle import codec as ocodec
+    from tests.conftest import u16
+    m = _model(kind)
+    ids = _ids(seed=21)
+    eng = exactkv.Engine(m, B, PROMPT + NEW, backend="exactkv")
+    print(f"[engine] {kind}: write-through prefill vs oracle", flush=True)
+    eng.prefill(ids, fused=True)
+    ref = [[[], []] for _ in range(eng.L)]             # per layer: K, V of each sequence [T, H, D]
+    with torch.no_grad(), _fused_sdpa():
+        for b in range(B):
+            pkv = m.model(ids[b:b + 1], use_cache=True).past_key_values
+            for i in range(eng.L):
+                ref[i][0].append(pkv.layers[i].keys[0].transpose(0, 1).cpu())
+                ref[i][1].append(pkv.layers[i].values[0].transpose(0, 1).cpu())
+    torch.cuda.synchronize()
+    Tf = PROMPT // 16 * 16
+    for i in range(eng.L):
+        for c, xs in zip(eng.kv[i], ref[i]):
+            x = torch.stack(xs)                        # [B, T, H, D]
+            want = ocodec.encode(u16(x[:, :Tf]))
+            npg = Tf // 16
+            for name, t in (("sm", c.sm[:, :Tf]), ("code", c.code[:, :Tf]), ("base", c.base[:, :npg]),
+                            ("rowmask", c.rowmask[:, :npg]), ("rowoff", c.rowoff[:, :npg])):
+                assert np.array_equal(t.cpu().numpy(), want[name]), (kind, i, name)
+            n = want["raw"].shape[0]
+            assert int(c.cnt.item()) == n, (kind, i)
+            assert np.array_equal(u16(c.raw[:n]), want["raw"]), (kind, i, "raw")
+            H = c.H
+            assert (c.rowmask[:, npg] == 0xFFFF).all()
+            slots = c.cap + torch.arange(B * H, device=c.raw.device, dtype=torch.int32).view(B, H) * 16
+            assert torch.equal(c.rowoff[:, npg], slots)
+            for b in range(B):
+                for h in range(H):
+                    s0 = c.cap + (b * H + h) * 16
+                    assert np.array_equal(u16(c.raw[s0: s0 + PROMPT - Tf]), u16(x[b, Tf:, h])), (kind, i, b, h)
+
+
 def test_sliding_window_model():
     """Qwen2 with sliding-window layers (use_sliding_window, window 24 < the 37-token
     prompt): both backends give bit-identical logits, and with teacher forcing they follow

@@ -134,3 +134,27 @@ def test_bad_blobs_raise():
         wire.unpack(blob, exactkv.CompressedKV(1, 64, 4, 128), 0)
     with pytest.raises(ValueError, match="shorter"):
         wire.unpack(blob[:-256].clone() if blob.numel() > 512 else blob[:300].clone(), c, 0)
+
+
+def test_unpack_skips_a_blob_whose_rowmask_disagrees_with_its_header(monkeypatch):
+    """The kernel's own check (behind the host's): a blob whose rowmask marks more raw rows
+    than its header declares is skipped on the device -- its sequence is not written and
+    the counter advances by the declared rows only -- while the blob before it unpacks."""
+    H = 4
+    x = synthetic.make_kv(2, 64, H, kind="k", seed=31, raw_row_rate=0.05)
+    src = _cache(x)
+    good, bad = wire.pack(src, 0), wire.pack(src, 1)
+    h = wire.header(bad)
+    rm = bad[h["off_rowmask"]: h["off_rowmask"] + 4 * h["full_pages"] * H].view(torch.int32)
+    rm[0] |= 0xFFFF                                     # every token of page 0, head 0 raw
+    with pytest.raises(ValueError, match="declares"):
+        wire.unpack_many([good, bad], exactkv.CompressedKV(2, src.TS, H, 128), [0, 1])
+    monkeypatch.setattr(wire, "_check_blob", lambda b, c: wire.header(b))   # past the host check
+    dst = exactkv.CompressedKV(2, src.TS, H, 128)
+    cnt0 = int(dst.cnt.item())
+    _say("wire corrupt blob", wire.header(good)["raw_rows"], h["raw_rows"])
+    wire.unpack_many([good, bad], dst, [0, 1])
+    torch.cuda.synchronize()
+    assert int(dst.cnt.item()) == cnt0 + wire.header(good)["raw_rows"] + h["raw_rows"]
+    assert same_bits(kernels.decode_to_bf16(dst.buffers(), 64)[0], x[0].to(DEV))
+    assert int(dst.sm[1].sum().item()) == 0 and int(dst.code[1].sum().item()) == 0

@@ -46,3 +46,11 @@ def test_malformed_blobs_are_rejected():
         H = 4
     with pytest.raises(ValueError, match="heads"):
         wire._check_blob(b, Four)
+
+    bad = b.clone()
+    h = wire.header(b)
+    assert h["full_pages"] > 0
+    rm = bad[h["off_rowmask"]: h["off_rowmask"] + 4 * h["full_pages"] * 2].view(torch.int32)
+    rm[0] ^= 1 << 15                                    # one more (or one less) raw row than declared
+    with pytest.raises(ValueError, match="declares"):
+        wire._check_blob(bad, _Cache)

@@ -25,6 +25,8 @@ SIGNATURES = {
     "exkv_cache_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _i64,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_bf16_append_paged": [_p, _i64, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p],
+    "exkv_cache_open_page": [_p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p],
+    "exkv_cache_open_pages_paged": [_p, _p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _i64, _i64, _i32, _p],
     "exkv_decode_to_bf16": [_p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p],
     "exkv_decode_to_bf16_paged": [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _p],
     "exkv_attn_compressed": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p,

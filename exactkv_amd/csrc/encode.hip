@@ -413,6 +413,37 @@ __global__ void bump_kernel(int32_t* state, int TS) {
     if (state[0] < TS) state[0] += 1;
 }
 
+// Opens the page that holds token state[0] of every (sequence, head): rowmask 0xFFFF and
+// rowoff = cap + (b * H + h) * 16, the (sequence, head)'s rows after the escaped-row slots.
+// The page index comes from the device token count, so the caches call it when they are
+// filled and after their raw pool moves, without indexing the page table on the host.
+// Nothing is written for a full cache (state[0] >= TS).
+__global__ void __launch_bounds__(256) open_page_kernel(int32_t* rowmask, int32_t* rowoff, const int32_t* state,
+                                                        int64_t cap, int B, int H, int TS) {
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    const int T = state[0];
+    if (u >= B * H || T < 0 || T >= TS) return;
+    const int64_t page = ((int64_t)(u / H) * (TS / kPage) + T / kPage) * H + u % H;
+    rowmask[page] = 0xFFFF;
+    rowoff[page] = (int32_t)(cap + (int64_t)u * kPage);
+}
+
+// Paged caches: the same for sequence slots slots[0 .. n): slot s's open page is table entry
+// lens[s] / 16 (when it exists), its rows at cap + (s * H + h) * 16.
+__global__ void __launch_bounds__(256) open_pages_paged_kernel(int32_t* rowmask, int32_t* rowoff,
+                                                               const int32_t* slots, int n, const int32_t* lens,
+                                                               const int32_t* bt, int64_t bt_stride, int max_seqs,
+                                                               int max_pages, int pool_pages, int64_t cap, int H) {
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= n * H) return;
+    const int s = (int)min((uint32_t)slots[u / H], (uint32_t)(max_seqs - 1)), h = u % H;
+    const int T = lens[s];
+    if (T < 0 || T / kPage >= max_pages) return;
+    const int64_t pidx = min((uint32_t)bt[s * bt_stride + T / kPage], (uint32_t)(pool_pages - 1));
+    rowmask[pidx * H + h] = 0xFFFF;
+    rowoff[pidx * H + h] = (int32_t)(cap + ((int64_t)s * H + h) * kPage);
+}
+
 // ---------------------------------------------------------------- paged append
 
 // One token for each of n sequences held in a pool of pages. Sequence slot s (batch row i
@@ -677,6 +708,34 @@ extern "C" int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void*
                        (const uint16_t*)x, sx_b, sx_h, (uint16_t*)buf, (const int32_t*)state, B, H, TS);
     hipLaunchKernelGGL(bump_kernel, dim3(1), dim3(1), 0, stream, state, TS);
     return launch_status("bf16_append");
+}
+
+extern "C" int exkv_cache_open_page(int32_t* rowmask, int32_t* rowoff, const int32_t* state, int64_t cap,
+                                    int64_t raw_rows, int32_t B, int32_t H, int32_t TS, hipStream_t stream) {
+    EXKV_REQUIRE(TS > 0 && TS % kPage == 0 && B > 0 && H > 0, "open_page: bad shape B=%d H=%d TS=%d", B, H, TS);
+    EXKV_REQUIRE(cap >= 0 && cap + (int64_t)B * H * kPage <= raw_rows && cap + (int64_t)B * H * kPage <= INT32_MAX,
+                 "open_page: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
+    EXKV_REQUIRE(rowmask && rowoff && state, "open_page: null pointer");
+    hipLaunchKernelGGL(open_page_kernel, dim3((unsigned)((B * H + 255) / 256)), dim3(256), 0, stream, rowmask,
+                       rowoff, state, cap, B, H, TS);
+    return launch_status("cache_open_page");
+}
+
+extern "C" int exkv_cache_open_pages_paged(int32_t* rowmask, int32_t* rowoff, const int32_t* slots, int32_t n,
+                                           const int32_t* lens, const int32_t* block_table, int64_t bt_stride,
+                                           int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int64_t cap,
+                                           int64_t raw_rows, int32_t H, hipStream_t stream) {
+    EXKV_REQUIRE(n >= 0 && n <= max_seqs && H > 0 && max_pages > 0 && bt_stride >= max_pages && pool_pages > 0,
+                 "open_pages_paged: bad shape n=%d H=%d max_seqs=%d max_pages=%d", n, H, max_seqs, max_pages);
+    EXKV_REQUIRE(cap >= 0 && cap + (int64_t)max_seqs * H * kPage <= raw_rows &&
+                     cap + (int64_t)max_seqs * H * kPage <= INT32_MAX,
+                 "open_pages_paged: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
+    EXKV_REQUIRE(rowmask && rowoff && lens && block_table && (slots || n == 0), "open_pages_paged: null pointer");
+    if (n == 0) return EXKV_OK;
+    hipLaunchKernelGGL(open_pages_paged_kernel, dim3((unsigned)((n * H + 255) / 256)), dim3(256), 0, stream,
+                       rowmask, rowoff, slots, n, lens, block_table, bt_stride, max_seqs, max_pages, pool_pages, cap,
+                       H);
+    return launch_status("cache_open_pages_paged");
 }
 
 static int check_paged_append(const char* what, int32_t n, int32_t H, int32_t D, int32_t max_seqs,

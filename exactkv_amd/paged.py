@@ -24,6 +24,7 @@ compact().
 """
 import torch
 
+from . import _lib
 from .kernels import P, encode_pages_paged, append_paged, append_paged_bf16
 
 
@@ -182,38 +183,46 @@ class PagedCompressedKV:
 
     # -- internals
     def _tail(self, slot):
-        """bf16 [H, 16, D] view of a slot's open page."""
-        o = self.cap + slot * self.H * P
-        return self.raw[o: o + self.H * P].view(self.H, P, self.D)
-
-    def _tail_rows(self, slot):
-        return self.cap + slot * self.H * P + torch.arange(self.H, dtype=torch.int32, device=self.dev) * P
+        """bf16 [H, 16, D] view of a slot's open page (its rows behind cap)."""
+        first = self.cap + slot * self.H * P
+        return self.raw.narrow(0, first, self.H * P).view(self.H, P, self.D)
 
     def _buf(self):
-        return dict(sm=self.sm, code=self.code, base=self.base, rowmask=self.rowmask, rowoff=self.rowoff,
-                    raw=self.raw, cnt=self.cnt, before=self._before, cap=self.cap, TS=self.TS, H=self.H, D=self.D)
+        """The encoder's view (kernels.encode_pages_paged): arrays, counters and sizes."""
+        d = {k: getattr(self, k) for k in ("sm", "code", "base", "rowmask", "rowoff", "raw")}
+        d.update(cnt=self.cnt, before=self._before, cap=self.cap, TS=self.TS, H=self.H, D=self.D)
+        return d
 
-    def _open(self, slot, T):
-        if T // P < self.table.max_pages:
-            pg = self.table._pages[slot][T // P]
-            self.rowmask[0, pg] = (1 << P) - 1
-            self.rowoff[0, pg] = self._tail_rows(slot)
+    def _open(self, slots):
+        """Open the page after the last full page of each of `slots` (host ints) -- table entry
+        lens[s] // 16, rows behind cap -- on the device, from the table's device lengths."""
+        t = self.table
+        if not slots:
+            return
+        sl = torch.tensor(slots, dtype=torch.int32).to(self.dev)
+        bt = t.block_table
+        _lib.call("exkv_cache_open_pages_paged", _lib.ptr(self.rowmask, 4), _lib.ptr(self.rowoff, 4),
+                  _lib.ptr(sl, 4), len(slots), _lib.ptr(t.lens, 4), _lib.ptr(bt, 4), bt.stride(0), t.max_seqs,
+                  t.max_pages, t.num_pages, self.cap, self.raw.shape[0], self.H, _lib.stream())
 
     def _grow(self, need):
-        new_cap = max(2 * self.cap, need + self.cap // 4)
-        raw = torch.zeros(new_cap + self._step_room, self.D, dtype=torch.bfloat16, device=self.dev)
-        raw[: self.cap] = self.raw[: self.cap]
-        raw[new_cap:] = self.raw[self.cap:]
-        self.raw, self.cap = raw, new_cap
+        """Room for `need` escaped rows: capacity max(2 cap, need + cap/4) (the contiguous
+        cache's rule); the open-page rows move behind the new capacity and every live slot's
+        open page is re-pointed on the device."""
+        old, cap = self.cap, max(2 * self.cap, need + self.cap // 4)
+        pool = torch.zeros((cap + self._step_room, self.D), dtype=torch.bfloat16, device=self.dev)
+        pool[:old].copy_(self.raw[:old])
+        pool[cap:].copy_(self.raw[old:])
+        self.raw, self.cap = pool, cap
         self.grows += 1
-        for s in self.table.live_slots():                     # open pages point into the moved tail area
-            self._open(s, self.table.length(s))
+        self._open(self.table.live_slots())
 
-    def _ensure_headroom(self, cnt):
-        if self.cap - cnt < self._step_room:
-            self._grow(cnt + self._step_room)
-            return True
-        return False
+    def _keep_headroom(self, cnt):
+        """Grow unless one more step of every slot and head fits behind `cnt` rows."""
+        if self.cap - cnt >= self._step_room:
+            return False
+        self._grow(cnt + self._step_room)
+        return True
 
     def _encode_pages(self, src, st, dst, npg):
         encode_pages_paged(src, st, self._buf(), dst, 1, npg)
@@ -238,10 +247,10 @@ class PagedCompressedKV:
                 assert n <= self.cap
         else:
             n = int(self.cnt.item())
-        self._open(slot, T)
+        self._open([slot])
         if T > Tf:
             self._tail(slot)[:, : T - Tf] = x[0, Tf:].transpose(0, 1)
-        self._ensure_headroom(n)
+        self._keep_headroom(n)
 
     prefill_slot = prefill                     # the write-through prefill calls this name
 
@@ -285,7 +294,7 @@ class PagedCompressedKV:
             grew = True
         self._pending = None
         if cnt is not None:
-            grew |= self._ensure_headroom(cnt)
+            grew |= self._keep_headroom(cnt)
         return grew
 
     def compact(self):

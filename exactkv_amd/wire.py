@@ -185,4 +185,4 @@ def unpack_many(blobs, cache, seqs):
               d["pages"].data_ptr(), width, d["tokens"].data_ptr(), d["open"].data_ptr(), d["tails"].data_ptr(),
               d["blobs"].data_ptr(), d["sizes"].data_ptr(), max_t, cache.H, cache.D, d["ws"].data_ptr(), ws_stride,
               _lib.stream())
-    cache._ensure_headroom(cnt + N)
+    cache._keep_headroom(cnt + N)

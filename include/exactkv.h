@@ -104,6 +104,25 @@ int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf,
                            int32_t H, int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
                            hipStream_t stream);
 
+/* Open the page holding token state[0] (device) of every (sequence, head) of a contiguous
+ * compressed cache: rowmask = 0xFFFF, rowoff = cap + (b * H + h) * 16 (its rows in the
+ * tail area after the cap escaped-row slots). Nothing when state[0] >= TS. Called when a
+ * cache is filled and after its raw pool moves (growth), so the page index and offsets are
+ * worked out on the device.
+ * Replaces: cache.py:54-56 _open_tail and the open-page fix-up of cache.py:70-71 (host-side
+ * indexing of rowmask / rowoff by the host token count). */
+int exkv_cache_open_page(int32_t* rowmask, int32_t* rowoff, const int32_t* state, int64_t cap, int64_t raw_rows,
+                         int32_t B, int32_t H, int32_t TS, hipStream_t stream);
+
+/* The same for a paged cache: for each sequence slot s = slots[i] (i < n), table entry
+ * lens[s] / 16 (if < max_pages) of block_table is opened with its rows at
+ * cap + (s * H + h) * 16. No counterpart in the reference (contiguous caches only; see
+ * exkv_cache_append_paged). */
+int exkv_cache_open_pages_paged(int32_t* rowmask, int32_t* rowoff, const int32_t* slots, int32_t n,
+                                const int32_t* lens, const int32_t* block_table, int64_t bt_stride, int32_t max_seqs,
+                                int32_t max_pages, int32_t pool_pages, int64_t cap, int64_t raw_rows, int32_t H,
+                                hipStream_t stream);
+
 /* Wire form of a sequence's compressed cache: one contiguous little-endian blob
  *   header  256 B: u32 magic 0x564B5845 ("EXKV"), version 1, heads H, head_dim 128,
  *           tokens T, full_pages T/16, tail_rows T%16, raw_rows N; u64 off_tail,

@@ -116,6 +116,48 @@ def time_calls(fn, n, warmup, copies):
     return t[n // 2], t[n // 10], t[(9 * n) // 10]
 
 
+def _hip():
+    """The HIP runtime torch has loaded (for raw event calls)."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+def time_split_kernel(launch, n, warmup, copies):
+    """Average and median ms of the split kernel itself: each of n launches (rotating over
+    `copies` inputs, back to back) records a pair of HIP events at the kernel's own start
+    and end on its launch stream (exkv_time_next_split, hipExtLaunchKernelGGL)."""
+    import ctypes
+    import torch
+    from exactkv_amd import _lib
+    lib, hip = _lib.load(), _hip()
+    for i in range(warmup):
+        launch(i % copies)
+    torch.cuda.synchronize()
+    ev = []
+    for _ in range(2 * n):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        ev.append(e)
+    for i in range(n):
+        lib.exkv_time_next_split(ev[2 * i], ev[2 * i + 1])
+        launch(i % copies)
+    torch.cuda.synchronize()
+    t = []
+    for i in range(n):
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[2 * i], ev[2 * i + 1]) == 0
+        t.append(ms.value)
+    for e in ev:
+        hip.hipEventDestroy(e)
+    t.sort()
+    return sum(t) / n, t[n // 2]
+
+
 def time_graph(fn, n, warmup, copies, per_graph=20):
     """Average ms per call of fn(i) with the calls captured in a HIP graph (per_graph calls
     rotating over `copies` inputs) and the graph replayed until n calls ran: the launch
@@ -146,39 +188,45 @@ def time_graph(fn, n, warmup, copies, per_graph=20):
     return e0.elapsed_time(e1) / (reps * per_graph)
 
 
-def cpu_baseline(kc, vc, q, B, T, nseq, min_seconds):
-    """The oracle (restated reference codec decode + fp32 GQA attention, numpy, 1 thread) on
-    the first `nseq` sequences, repeated until at least `min_seconds` of CPU work; reported
-    as microseconds for the full B-sequence call."""
-    import numpy as np
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on."""
+    return len(os.sched_getaffinity(0))
+
+
+def host_cache(c, nseq=None):
+    """A compressed cache's six tensors and shape as CPU tensors (the first nseq sequences)."""
     import torch
-    from threadpoolctl import threadpool_limits
+    d = {k: (getattr(c, k)[:nseq] if nseq else getattr(c, k)).cpu() for k in ("sm", "code", "base", "rowmask", "rowoff")}
+    d["raw"] = c.raw.cpu()
+    d["shape"] = (nseq or c.B, c.TS, c.H, c.D)
+    return d
 
-    from oracle import attention as oatt
-    from oracle import codec as ocodec
 
-    def host(c):
-        d = dict(shape=(nseq, c.TS, c.H, c.D))
-        for k in ("sm", "code", "base", "rowmask", "rowoff"):
-            d[k] = getattr(c, k)[:nseq].cpu().numpy()
-        d["raw"] = c.raw.cpu().view(torch.int16).numpy().view(np.uint16)
-        return d
-    hk, hv = host(kc), host(vc)
-    qh = q[:nseq].cpu().view(torch.int16).numpy().view(np.uint16)
-    reps = 0
-    with threadpool_limits(limits=1):
+def median_seconds(fn, runs):
+    """Median and minimum wall time of `runs` calls of fn (time.perf_counter)."""
+    ts = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        while True:
-            kd = ocodec.decode(hk, T)
-            vd = ocodec.decode(hv, T)
-            oatt.attention(qh, kd, vd, T, np.float32)
-            reps += 1
-            dt = time.perf_counter() - t0
-            if dt >= min_seconds:
-                break
-    return dict(value=round(dt / reps * 1e6 * B / nseq, 1), unit="us", cores=1, kind="port",
-                sample=f"{reps} passes over {nseq} of {B} sequences x {T} tokens: numpy codec decode of K and V "
-                       f"+ fp32 attention, per pass scaled x{B / nseq:g}", cpu=cpu_model(), seconds=round(dt, 2))
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts[0]
+
+
+def cpu_baseline(kc, vc, q, B, T, runs, lens=None):
+    """The reference codec restated in PyTorch (oracle.torch_codec, byte-identical to
+    codec.py) decoding both caches, then fp32 GQA attention, on every host core this process
+    may use; the median of `runs` full calls, in microseconds."""
+    import torch
+    from oracle import torch_codec
+    n = cpu_threads()
+    torch.set_num_threads(n)
+    hk, hv, hq = host_cache(kc), host_cache(vc), q.cpu()
+    med, best = median_seconds(lambda: torch_codec.decode_attention(hq, hk, hv, T, lens=lens), runs)
+    return dict(value=round(med * 1e6, 1), unit="us", cores=n, kind="port",
+                sample=f"median of {runs} full calls on the same caches ({B} x {T} tokens): torch restatement "
+                       f"of the reference codec decoding K and V, then fp32 GQA attention",
+                min_us=round(best * 1e6, 1), cpu=cpu_model(), torch_threads=torch.get_num_threads())
 
 
 def main():
@@ -194,8 +242,7 @@ def main():
     ap.add_argument("--e2e-work-gib", type=float, default=6.0,
                     help="memory kept free beyond the caches for activations, logits and pool growth")
     ap.add_argument("--copies", type=int, default=4, help="cache copies rotated to defeat the 256 MB MALL")
-    ap.add_argument("--cpu-seqs", type=int, default=8)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="minimum CPU work of the baseline sample")
+    ap.add_argument("--cpu-runs", type=int, default=5, help="CPU baseline: median of this many runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--target-blocks", type=int, default=None)
     ap.add_argument("--window", type=int, default=0,
@@ -260,10 +307,10 @@ def main():
 
     ms_c = time_loop(full_c, a.steps, a.warmup, a.copies)
     ms_b = time_loop(full_b, a.steps, a.warmup, a.copies)
-    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True, window=W), a.steps,
-                         a.warmup, a.copies)
-    ms_split_b = time_loop(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False, window=W), a.steps,
-                           a.warmup, a.copies)
+    ms_split, ms_split_med = time_split_kernel(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True,
+                                                                    window=W), max(a.steps, 50), a.warmup, a.copies)
+    ms_split_b, _ = time_split_kernel(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False, window=W),
+                                      max(a.steps, 50), a.warmup, a.copies)
     ms_c_graph = time_graph(full_c, a.steps, a.warmup, a.copies)
     med, p10, p90 = time_calls(full_c, max(a.steps, 50), a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
@@ -271,7 +318,7 @@ def main():
     alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv, window=W)
     alg_b = 2 * B * min(T, W or T) * Hkv * 256 + 2 * B * Hq * 128 * 2
     gbps = alg / (ms_split * 1e-3) / 1e9
-    enc = encoder_gbps(exactkv, kernels, kbs[0], T, a.steps, a.warmup)
+    enc = encoder_gbps(exactkv, kernels, kbs[:2], T, a.steps, a.warmup)
     print("[bench] encoder timed", file=sys.stderr, flush=True)
 
     traffic, traffic_src = profiled_traffic(a.workload) if not W else (None, None)
@@ -285,7 +332,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
-                     "kernel_us": round(ms_split * 1e3, 2)},
+                     "kernel_us": round(ms_split * 1e3, 2), "kernel_us_median": round(ms_split_med * 1e3, 2),
+                     "kernel_timing": "HIP events recorded at each split kernel's own start and end "
+                                      "(hipExtLaunchKernelGGL) on its launch stream, back-to-back launches"},
         "timing": "HIP events around back-to-back calls on one stream",
         "graph_replay_us": round(ms_c_graph * 1e3, 2),
         "per_call_us": {"median": round(med * 1e3, 2), "p10": round(p10 * 1e3, 2), "p90": round(p90 * 1e3, 2),
@@ -300,7 +349,7 @@ def main():
         "gpu": torch.cuda.get_device_name(0),
     }
     if not a.no_cpu_baseline and not W:                # the baseline is the full-context attention
-        res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, min(a.cpu_seqs, B), a.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, a.cpu_runs)
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
 
@@ -343,8 +392,8 @@ def paged_c2a(a):
                                                             out=out, block_table=bts[i]), a.steps, a.warmup, a.copies)
     ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out,
                                                            block_table=bts[i]), a.steps, a.warmup, a.copies)
-    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True, block_table=bts[i]),
-                         a.steps, a.warmup, a.copies)
+    ms_split, _ = time_split_kernel(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True,
+                                                         block_table=bts[i]), max(a.steps, 50), a.warmup, a.copies)
     # algorithmic bytes: those of the gathered pages (the table's pages of the pool)
     alg = 0
     for c in (kcs[0], vcs[0]):
@@ -441,10 +490,10 @@ def wire_bench(a):
         x0 = raw_src[0].cpu().view(torch.int16).numpy().view(np.uint16)
         t0 = time.perf_counter()
         n = 0
-        while True:                                    # one sequence's K at a time, >= cpu-seconds / 4
+        while True:                                    # one sequence's K at a time, >= 3 s
             owire.pack(x0)
             n += 1
-            if time.perf_counter() - t0 >= a.cpu_seconds / 4:
+            if time.perf_counter() - t0 >= 3.0:
                 break
         per_seq = (time.perf_counter() - t0) / n
         cpu = {"value": round(2 * sizes[0][0] / per_seq / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
@@ -502,7 +551,7 @@ def c3_stress(a):
     k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=100, device=dev, raw_row_rate=6e-3)
     v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=101, device=dev, raw_row_rate=6e-3)
     q = synthetic.make_q(B, Hq, seed=102, device=dev)
-    enc = encoder_gbps(exactkv, kernels, k, TS, a.steps, a.warmup)
+    enc = encoder_gbps(exactkv, kernels, [k, v], TS, a.steps, a.warmup)
     print("[c3] encoder timed", file=sys.stderr, flush=True)
     kcs, vcs, kbs, vbs, grows = [], [], [], [], []
     for i in range(a.copies):
@@ -528,8 +577,8 @@ def c3_stress(a):
                                                             out=out), a.steps, a.warmup, a.copies)
     ms_b = time_loop(lambda i: kernels.attention_reference(q, kbs[i], vbs[i], TS, lens=ld, nsplit=ns, split_len=sl,
                                                            out=out), a.steps, a.warmup, a.copies)
-    ms_split = time_loop(lambda i: split_only(kernels, q, kcs[i], vcs[i], TS, ns, sl, True, ld), a.steps, a.warmup,
-                         a.copies)
+    ms_split, _ = time_split_kernel(lambda i: split_only(kernels, q, kcs[i], vcs[i], TS, ns, sl, True, ld),
+                                    max(a.steps, 50), a.warmup, a.copies)
     alg = algorithmic_bytes([kcs[0], vcs[0]], B, TS, Hq, Hkv, lens)
     gbps = alg / (ms_split * 1e-3) / 1e9
     res = {
@@ -782,22 +831,33 @@ def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table
                   wl.data_ptr(), B, Hq, Hkv, D, T, TS, lp, lstride, ns, sl, window, scale, _lib.stream())
 
 
-def encoder_gbps(exactkv, kernels, x, T, steps, warmup):
-    """Page-encoder throughput on one prefill of the workload's keys: (bf16 read + compressed
-    write) bytes / time."""
+def encoder_gbps(exactkv, kernels, xs, T, steps, warmup):
+    """Page-encoder throughput over a prefill of the workload's keys: (bf16 read + compressed
+    write) bytes / time, alternating between len(xs) sources and as many caches so that the
+    working set (> 256 MB at c2a and c3) is not held by the 256 MB Infinity Cache. Each cache's
+    pool has room for every timed encode, so the raw-row counter is never reset inside the
+    timed region and every raw row is written."""
     import torch
-    B, TS, H, D = x.shape
+    B, TS, H, D = xs[0].shape
     npg = T // 16
-    c = exactkv.CompressedKV(B, TS, H, D, reserve=0.05)
-    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    st = (xs[0].stride(0), 16 * xs[0].stride(1), xs[0].stride(1), xs[0].stride(2))
+    n = max(5, steps // 5)
+    raw = []
+    for x in xs:                                       # raw rows one encode of each source writes
+        probe = exactkv.CompressedKV(B, TS, H, D, reserve=0.05)
+        kernels.encode_pages(x, st, probe._buf(), 0, 0, B, npg)
+        raw.append(int(probe.cnt.item()))
+        del probe
+    reps = n + warmup
+    caches = [exactkv.CompressedKV(B, TS, H, D, reserve=(reps * max(r, 1) * 2.0) / (B * TS * H)) for r in raw]
 
-    def enc(_):
-        c.cnt.zero_()
-        kernels.encode_pages(x, st, c._buf(), 0, 0, B, npg)
-    ms = time_loop(enc, max(5, steps // 5), max(2, warmup // 5), 1)
-    nraw = int(c.cnt.item())
+    def enc(i):
+        kernels.encode_pages(xs[i], st, caches[i]._buf(), 0, 0, B, npg)
+    ms = time_loop(enc, n, warmup, len(xs))
+    torch.cuda.synchronize()
+    assert all(int(c.cnt.item()) <= c.cap for c in caches)
     rows = B * npg * 16 * H
-    byts = rows * 256 + rows * 192 + B * npg * H * 136 + nraw * 256
+    byts = rows * 256 + rows * 192 + B * npg * H * 136 + sum(raw) / len(raw) * 256
     return round(byts / (ms * 1e-3) / 1e9, 1)
 
 

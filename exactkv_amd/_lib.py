@@ -51,6 +51,7 @@ SIGNATURES = {
     "exkv_wire_unpack": [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _i32,
                          _i32, _i32, _p, _i64, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
+    "exkv_time_next_split": [_p, _p],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],
     "exkv_last_error": [],

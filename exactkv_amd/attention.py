@@ -1,18 +1,23 @@
-"""Decode attention over either cache type, for one query token per sequence
-(drop-in for the reference's exactkv/attention.py:6-15)."""
+"""decode_attention: one decode step's attention over whichever cache holds the keys and
+values (the reference's entry point, exactkv/attention.py:6-15, same name and arguments)."""
 from .cache import CompressedKV, BF16KV
 from .paged import PagedCompressedKV, PagedBF16KV
 from .kernels import attention_compressed, attention_reference
 
 
 def decode_attention(q, k_cache, v_cache, **kw):
-    """q: [B, Hq, D] bf16 contiguous (after RoPE). k_cache / v_cache: both CompressedKV or both BF16KV
-    (or both PagedCompressedKV / PagedBF16KV of one PageTable, q row i being the current
-    step's slot i), already holding the current token. Returns [B, Hq, D] bf16.
+    """Attention of one new query token per sequence over its cached keys and values.
 
-    The two cache types give bit-identical results for the same contents and split plan."""
+    q: bf16 [B, Hq, 128], contiguous, RoPE already applied. k_cache / v_cache: a matching
+    pair -- CompressedKV, BF16KV, or PagedCompressedKV / PagedBF16KV of one PageTable (then
+    row i of q belongs to the current step's slot i) -- whose appends for this step have
+    already run, so the current token is attended to. Extra keywords go to the kernel call
+    (window=, nsplit=, split_len=, out=, ...). Returns bf16 [B, Hq, 128].
+
+    A compressed pair and a bf16 pair holding the same tokens return the same bits for the
+    same split plan. Any other cache type raises TypeError."""
     if isinstance(k_cache, (PagedCompressedKV, PagedBF16KV)):
-        _, bt, lens = k_cache.table.step_rows()          # row i of q is the step's slot i
+        _, bt, lens = k_cache.table.step_rows()
         if isinstance(k_cache, PagedCompressedKV):
             return attention_compressed(q, k_cache.buffers(), v_cache.buffers(), 0, lens=lens, block_table=bt, **kw)
         return attention_reference(q, k_cache.buf, v_cache.buf, 0, lens=lens, block_table=bt, **kw)

@@ -29,6 +29,8 @@
 //     needs no cross-lane traffic.
 // Everything after the K/V rebuild is shared by the two kernels, so the compressed and
 // uncompressed results are identical bit for bit.
+#include <hip/hip_ext.h>
+
 #include "tile.hpp"
 #include "../../include/exactkv.h"
 
@@ -96,6 +98,9 @@ __device__ inline bool raw_in_ring(const PageMeta& m) {
     const int n = raw_rows_of(m);
     return n > 0 && n <= kRawRing;
 }
+// Loads a compressed page takes: its 7 byte loads, plus one raw-row load when its raw rows
+// travel through the ring
+__device__ inline int raw_loads(const PageMeta& m) { return raw_in_ring(m) ? 1 : 0; }
 
 struct AttnArgs {
     const uint16_t* q;        // [B, Hq, 128] bf16
@@ -255,6 +260,18 @@ __device__ inline void wait_vm() {
 }
 
 
+// wait_vm with a wave-uniform count of 0, 1, 7 or 8 loads
+__device__ inline void wait_vm_n(int n) {
+    if (n >= 8)
+        wait_vm<8>();
+    else if (n == 7)
+        wait_vm<7>();
+    else if (n == 1)
+        wait_vm<1>();
+    else
+        wait_vm<0>();
+}
+
 // Per-lane parts of a page's DMA addresses (fixed for the kernel): byte offsets from the
 // page's first row in each array, with the XOR swizzle of the destination applied.
 struct DmaLane {
@@ -285,15 +302,12 @@ __device__ inline DmaLane dma_lane_offsets(int lane, int64_t rs) {
     return o;
 }
 
-// Issue one page's kDmaPerPage loads into stage st. row0: row index of the page's token 0
-// ((b*TS + 16*pg)*Hkv + hk); page: its page index. The compressed page's raw-row load comes
-// last and is always issued (one lane, 16 bytes of the pool's first row, when the page has
-// none in the ring), so every page is the same number of loads and only the raw load waits
-// for the page's rowmask / rowoff.
+// Issue the byte loads of one page into stage st (7 for the compressed cache, 8 for bf16).
+// row0: row index of the page's token 0 ((b*TS + 16*pg)*Hkv + hk); page: its page index.
+// They need no page metadata, so the first pages' loads can leave before the page table.
 template <bool COMP>
-__device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row0, int64_t page, uint32_t st,
-                                int lane, const PageMeta& m, uint32_t raw_st, const PairSrc& basep,
-                                const PairSrc& rawp, const PairSrc& rawn) {
+__device__ inline void dma_page_bytes(const AttnArgs& a, const DmaLane& o, int64_t row0, int64_t page, uint32_t st,
+                                      int lane, const PairSrc& basep) {
     if constexpr (COMP) {
         const uint8_t* ksm = a.k.sm + row0 * 128;
         const uint8_t* vsm = a.v.sm + row0 * 128;
@@ -306,17 +320,6 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
         // base rows: lanes 0-7 K, 8-15 V
         const uint64_t bsrc = basep.pick((lane & 8) != 0) + (uint64_t)page * 128 + o.base;
         if (lane < 16) dma16((const void*)(uintptr_t)bsrc, st + CS_BASE);
-        // raw rows of the page (K rows in token order, then V rows): entry e = lane / 16 of
-        // at most kRawRing, 16 bytes per lane; pool index = rowoff + rank of the row
-        const int nk = __builtin_popcount(m.mk);
-        const int n = raw_in_ring(m) ? nk + __builtin_popcount(m.mv) : 0, e = lane >> 4;
-        const bool isv = e >= nk;
-        int64_t idx = n == 0 ? 0 : (isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e);
-        const int64_t rows = (int64_t)rawn.pick(isv);
-        idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
-        const uint64_t rb = rawp.pick(isv);
-        if (lane < (n == 0 ? 1 : 16 * n))
-            dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
     } else {
         const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.kb) + row0 * 256;
         const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.vb) + row0 * 256;
@@ -325,6 +328,29 @@ __device__ inline void dma_page(const AttnArgs& a, const DmaLane& o, int64_t row
             dma16(kp + o.bf_k[j], st + BS_K + j * 1024);
             dma16(vp + o.bf_v[j], st + BS_V + j * 1024);
         }
+    }
+}
+
+// The compressed page's raw-row load, issued only for a page whose raw rows travel through
+// the ring (raw_loads: the waits count it); the only load that needs the page's metadata.
+__device__ inline void dma_page_raw(int lane, const PageMeta& m, uint32_t raw_st, const PairSrc& rawp,
+                                    const PairSrc& rawn) {
+    if (!raw_in_ring(m)) return;                       // uniform
+    // the slot was last read by this wavefront's splice of two pages back: those LDS reads
+    // finish before the DMA can land there
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    {
+        // raw rows of the page (K rows in token order, then V rows): entry e = lane / 16 of
+        // at most kRawRing, 16 bytes per lane; pool index = rowoff + rank of the row
+        const int nk = __builtin_popcount(m.mk);
+        const int n = nk + __builtin_popcount(m.mv), e = lane >> 4;
+        const bool isv = e >= nk;
+        int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
+        const int64_t rows = (int64_t)rawn.pick(isv);
+        idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+        const uint64_t rb = rawp.pick(isv);
+        if (lane < 16 * n)
+            dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
     }
 }
 
@@ -552,12 +578,16 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         return PageMeta{(uint32_t)__builtin_amdgcn_readlane((int)vmk, j), (uint32_t)__builtin_amdgcn_readlane((int)vmv, j),
                         __builtin_amdgcn_readlane(vok, j), __builtin_amdgcn_readlane(vov, j)};
     };
-    PageMeta m0{0u, 0u, 0, 0}, m1{0u, 0u, 0, 0};
-    auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
+    auto issue_bytes = [&](int j, uint32_t sb) {
         const int64_t gp = gpage(j);
-        const int64_t row0 = gp * kPage * rs + hk;
-        const int64_t page = gp * rs + hk;
-        dma_page<COMP>(a, dl, row0, page, sb, lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), basep, rawp, rawn);
+        dma_page_bytes<COMP>(a, dl, gp * kPage * rs + hk, gp * rs + hk, sb, lane, basep);
+    };
+    auto issue_raw = [&](int j, const PageMeta& m) {
+        if constexpr (COMP) dma_page_raw(lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), rawp, rawn);
+    };
+    auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
+        issue_bytes(j, sb);
+        issue_raw(j, m);
     };
     // q through the last stage, which no page uses before page NST - 1 is issued
     const int gh = min(16, a.G - hg * 16);
@@ -571,8 +601,6 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    if (COMP && npw > 0) m0 = meta_s(0);
-    if (COMP && npw > 1) m1 = meta_s(1);
     q_dma(a, b, hk, hg, gh, lane, qst);
     if constexpr (COMP) {
         const int i = min(lane, max(npw - 1, 0));     // per lane: the wavefront's page i
@@ -584,14 +612,17 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         dma4(a.v.rowmask + page, mst + 512u);
         dma4(a.v.rowoff + page, mst + 768u);
     }
-    if (npw > 0) issue(0, ring, m0);
-    if (NST == 3 && npw > 1) issue(1, ring + STB, m1);
-    // q has landed once only the first pages' loads are in flight
+    // the first pages' bytes go out before their metadata is known: their raw-row loads follow
+    // once the page table has landed, so no scalar round trip sits before the first loads
+    if (npw > 0) issue_bytes(0, ring);
+    if (NST == 3 && npw > 1) issue_bytes(1, ring + STB);
+    // q and the page table have landed once only the first pages' byte loads are in flight
+    constexpr int kBytesPerPage = COMP ? kDmaPerPage[1] - 1 : kDmaPerPage[0];
     const int first = min(npw, NST - 1);
     if (first >= 2)
-        wait_vm<2 * kDmaPerPage[COMP]>();
+        wait_vm<2 * kBytesPerPage>();
     else if (first == 1)
-        wait_vm<kDmaPerPage[COMP]>();
+        wait_vm<kBytesPerPage>();
     else
         wait_vm<0>();
     // Q^T as the B operand: column = head hg*16 + r of this KV head's group, k-block kc
@@ -615,13 +646,24 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         vov = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 768u + 4u * lane));
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers before their stage is reused
+    if constexpr (COMP) {
+        if (npw > 0) issue_raw(0, meta(0));
+        if (npw > 1) issue_raw(1, meta(1));
+    }
 
     progress[wave] = 0;
     int stg = 0;                                       // stage of page j (j % NST)
     for (int j = 0; j < npw; ++j) {
-        // stage j is complete once only page j + 1's loads are in flight
+        // stage j is complete once only page j + 1's loads are in flight. The prologue issued
+        // page 0's bytes, page 1's bytes, then their raw-row loads: page 0 is in once only
+        // page 1's raw-row load is (or, without a raw-row load of its own, page 1's bytes too).
         if (NST == 3 && j + 1 < npw) {
-            wait_vm<kDmaPerPage[COMP]>();
+            if constexpr (COMP) {
+                const int next = raw_loads(meta(j + 1));
+                wait_vm_n(j > 0 ? kDmaPerPage[1] - 1 + next : (raw_loads(meta(0)) ? next : kDmaPerPage[1] - 1 + next));
+            } else {
+                wait_vm<kDmaPerPage[COMP]>();
+            }
         } else {
             wait_vm<0>();
         }
@@ -631,32 +673,33 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         const int pg = p0 + phase + nphase * j;
         const int t0 = pg * kPage;
         const bool ragged = t0 + kPage > end || t0 < wlo;  // uniform: a split's last page, or the window's first
-        const bool row_valid = t0 + r < end && t0 + r >= wlo;
+        auto row_valid = [&]() { return t0 + r < end && t0 + r >= wlo; };
         const PageMeta mc = COMP ? meta(j) : PageMeta{0u, 0u, 0, 0};
 
-        // The next page's loads: the bf16 twin's at once; the compressed cache's once this
-        // page's raw rows are out of their slot, which page j + 2's raw rows reuse.
+        // The next page's byte loads go out at once, into the stage the previous page used
+        // (its last LDS reads are waited for first). The compressed page's raw-row load
+        // follows once this page's raw rows are out of their slot, which it reuses; the
+        // waits above count both.
         const PageMeta mn = COMP && j + NST - 1 < npw ? meta(j + NST - 1) : PageMeta{0u, 0u, 0, 0};
-        auto issue_next = [&]() {
-            if (j + NST - 1 < npw) {
-                // the recycled stage and raw slot were last read by this wavefront's LDS
-                // accesses: let them finish before the DMA can land there
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                issue(j + NST - 1, ring + (uint32_t)(stn * STB), mn);
-            }
-        };
-        if (!COMP) issue_next();
+        if (j + NST - 1 < npw) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_bytes(j + NST - 1, ring + (uint32_t)(stn * STB));
+        }
         // Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one, and
         // the older one's first loads are also served first: left alone it runs ahead and its
-        // partner finishes last. The one that is behind takes the higher priority.
-        if (j > 0) {
-            const int other = progress[wave ^ 4];
-            if (j < other)
-                __builtin_amdgcn_s_setprio(2);
-            else
-                __builtin_amdgcn_s_setprio(0);
-        }
+        // partner finishes last. The one that is behind takes the higher priority. The
+        // partner's count is read here (an unsynchronised hint: either value is fine) and
+        // used once the page's LDS reads are out, so its round trip overlaps theirs.
+        const int other = progress[wave ^ 4];
         progress[wave] = j;
+        auto set_priority = [&]() {
+            if (j > 0) {
+                if (j < other)
+                    __builtin_amdgcn_s_setprio(2);
+                else
+                    __builtin_amdgcn_s_setprio(0);
+            }
+        };
 
         // ---- K and V bytes out of the stage together; the V reads overlap the K rebuild
         uint32_t kd[16], vd[16];
@@ -665,6 +708,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             PageBytes pk, pv;
             stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
             stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
+            set_priority();
             const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
             rebuild_values(pk, kd);
             if (mc.mk != 0) {                          // page with raw K rows
@@ -673,7 +717,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
             if (ragged) {                              // rows past the end of the split: zero
                 keep_branch();
-                if (!row_valid) {
+                if (!row_valid()) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) kd[i] = 0u;
                 }
@@ -690,18 +734,19 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
             if (ragged) {
                 keep_branch();
-                if (!row_valid) {
+                if (!row_valid()) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) vd[i] = 0u;
                 }
             }
+            if (j + NST - 1 < npw) issue_raw(j + NST - 1, mn);   // this page's raw rows are out of the slot
             write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
-            issue_next();
         } else {
             stage_bf16_k(sb, lo, kd);
+            set_priority();
             if (ragged) {
                 keep_branch();
-                if (!row_valid) {
+                if (!row_valid()) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) kd[i] = 0u;
                 }
@@ -712,7 +757,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
                     as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
             if (ragged) {                              // ragged last page: zero the V rows past the end
                 keep_branch();
-                if (!row_valid) {
+                if (!row_valid()) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) vd[i] = 0u;
                     write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
@@ -720,6 +765,14 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
         }
 
+        // V^T operands of this page's P.V MFMAs out of the V tile now (the tile's writes come
+        // first in the wavefront's LDS order), so their latency overlaps the softmax below.
+        s16x4 vt[8];
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const lds_u8* tp = lds_ptr(sb + lo.tr[nb & 3]) + Ring<COMP>::vtile + (nb >= 4 ? 128 : 0);
+            vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)tp);
+        }
         // The score MFMAs' result is read below after the branches above, whose opaque asm the
         // compiler's hazard tracking has counted as wait states (reads then saw stale
         // accumulators). Pass it through 16 explicit wait states instead: the asm defines sa,
@@ -727,13 +780,16 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         asm volatile("s_nop 7\n\ts_nop 7" : "+v"(sa));
         // ---- online softmax: lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
         // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into
-        // the exponent's fma: p = 2^(s * scale - m).
-        // Branch-free on purpose: with an opaque-asm branch between the MFMA and these reads,
-        // the compiler's hazard tracking has counted the asm as wait states and let the
-        // reads see the accumulators before the MFMA wrote them.
-        float sc[4];
+        // the exponent's fma: p = 2^(s * scale - m). Tokens outside the split or the window
+        // score -inf; only a ragged page has any (its branch follows the explicit wait
+        // states above, so the reads inside cannot see the accumulators early).
+        float sc[4] = {sa[0], sa[1], sa[2], sa[3]};
+        if (ragged) {
+            keep_branch();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = (t0 + 4 * g + i < end && t0 + 4 * g + i >= wlo) ? sa[i] : -INFINITY;
+            for (int i = 0; i < 4; ++i)
+                if (t0 + 4 * g + i >= end || t0 + 4 * g + i < wlo) sc[i] = -INFINITY;
+        }
         float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mloc = group_max(mloc) * a.qk_scale;
         const float m_new = fmaxf(m_i, mloc);
@@ -756,11 +812,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         // ---- O^T += V^T P^T: V^T rows 4g..4g+3 of channel 16nb + r via the transpose read
         const s16x4 pop = __builtin_bit_cast(s16x4, pb4);
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-            const lds_u8* tp = lds_ptr(sb + lo.tr[nb & 3]) + Ring<COMP>::vtile + (nb >= 4 ? 128 : 0);
-            const s16x4 av = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)tp);
-            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, pop, acc[nb], 0, 0, 0);
-        }
+        for (int nb = 0; nb < 8; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[nb], pop, acc[nb], 0, 0, 0);
     }
 
     // ---- merge the page phases of each head (same algebra as the split merge)
@@ -903,13 +955,31 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
     return EXKV_OK;
 }
 
+// Timing hook: events that the next split-kernel launch on this thread records at its start
+// and end (hipExtLaunchKernelGGL), consumed by that launch.
+static thread_local hipEvent_t t_split_start = nullptr, t_split_stop = nullptr;
+
 static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * (a.Hkv / a.HW) * a.HG));
-    if (comp)
+    hipEvent_t e0 = t_split_start, e1 = t_split_stop;
+    t_split_start = t_split_stop = nullptr;
+    if (e0 || e1) {
+        if (comp)
+            hipExtLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kThreads), 0, stream, e0, e1, 0, a);
+        else
+            hipExtLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kThreads), 0, stream, e0, e1, 0, a);
+    } else if (comp) {
         hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kThreads), 0, stream, a);
-    else
+    } else {
         hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kThreads), 0, stream, a);
+    }
     return hip_status(hipGetLastError(), comp ? "attn_split_compressed" : "attn_split_bf16");
+}
+
+extern "C" int exkv_time_next_split(hipEvent_t start, hipEvent_t stop) {
+    t_split_start = start;
+    t_split_stop = stop;
+    return EXKV_OK;
 }
 
 static int launch_reduce(const float* o, const float* m, const float* l, void* out, int64_t rows, int ns,

@@ -41,28 +41,29 @@ __host__ __device__ inline uint32_t bfi_b32(uint32_t m, uint32_t a, uint32_t b) 
 
 // ---------------------------------------------------------------- value rebuild
 //
-// Four consecutive channels at once. s: their sign|mantissa bytes; cn: their 4-bit
-// codes, one per byte (0..15); bm: their base bytes with the zero flag cleared
-// (0..127); zf: their base bytes' zero flags (0x80 per byte, 0 elsewhere).
-// Result: two dwords of bf16 pairs (channel c in the low half, c + 1 in the high half),
-// bit-identical to the reference decoder (codec.py:65-68, kernels.py:96-103).
+// Four consecutive channels at once. s: their sign|mantissa bytes; cn: their 4-bit codes,
+// one per byte (0..15); base: their base bytes. Without zero groups (HAS_ZERO_GROUPS false)
+// every base byte must be < 128. Result: two dwords of bf16 pairs (channel c in the low
+// half, c + 1 in the high half), bit-identical to the reference decoder (codec.py:65-68,
+// kernels.py:96-103).
 //
-// exponent e = bm + code (<= 142, so the bytewise add never carries). The bf16 is
+// exponent e = (base & 127) + code (<= 142, so the bytewise add never carries), or 0 in a
+// flagged group (base >= 128) where code == 0. The bf16 is
 // hi byte = (s & 0x80) | (e >> 1), lo byte = (e & 1) << 7 | (s & 0x7F).
-__host__ __device__ inline uint32_t zero_mask(uint32_t cn, uint32_t zf) {
-    // bit 7 of each byte of cn + 0x7F is set iff code >= 1 (code <= 15: no carry out)
-    uint32_t z80 = zf & ~(cn + 0x7F7F7F7Fu);
-    // 0x80 -> 0xFF per flagged byte: (z << 1) - (z >> 7) sets exactly those bytes
-    return (z80 << 1) - (z80 >> 7);
+__host__ __device__ inline uint32_t exponents(uint32_t cn, uint32_t base) {
+    // z80: bit 7 of a byte set iff its group is flagged and its code is 0 (code <= 15, so
+    // 0x80 - code keeps bit 7 exactly when code == 0); fm: 0x7F in those bytes, which
+    // clears the base there (the exponent is then the code, 0)
+    const uint32_t z80 = base & (0x80808080u - cn) & 0x80808080u;
+    const uint32_t fm = z80 - (z80 >> 7);
+    return (base & 0x7F7F7F7Fu & ~fm) + cn;
 }
 
 template <bool HAS_ZERO_GROUPS>
-__host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t bm, uint32_t zf,
-                                         uint32_t& out01, uint32_t& out23) {
-    uint32_t e = cn + bm;
-    if (HAS_ZERO_GROUPS) e &= ~zero_mask(cn, zf);
-    uint32_t lo = bfi_b32(0x7F7F7F7Fu, s, e << 7);
-    uint32_t hi = bfi_b32(0x80808080u, s, e >> 1);
+__host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t base, uint32_t& out01, uint32_t& out23) {
+    const uint32_t e = HAS_ZERO_GROUPS ? exponents(cn, base) : cn + base;
+    const uint32_t lo = bfi_b32(0x7F7F7F7Fu, s, e << 7);
+    const uint32_t hi = bfi_b32(0x80808080u, s, e >> 1);
     out01 = perm_b32(hi, lo, 0x05010400u);
     out23 = perm_b32(hi, lo, 0x07030602u);
 }

@@ -44,37 +44,35 @@ __device__ inline void load_page(const CSrc& c, int64_t row, int64_t page, int g
     pb.roff = c.rowoff[page];
 }
 
-template <bool Z>
-__device__ inline void rebuild_page_impl(const PageBytes& pb, uint32_t out[16]) {
-    const uint32_t S[4] = {pb.sm_lo.x, pb.sm_lo.y, pb.sm_lo.z, pb.sm_lo.w};
-    const uint32_t SH[4] = {pb.sm_hi.x, pb.sm_hi.y, pb.sm_hi.z, pb.sm_hi.w};
-    const uint32_t C[4] = {pb.code.x, pb.code.y, pb.code.z, pb.code.w};
-    const uint32_t BL[4] = {pb.b_lo.x, pb.b_lo.y, pb.b_lo.z, pb.b_lo.w};
-    const uint32_t BH[4] = {pb.b_hi.x, pb.b_hi.y, pb.b_hi.z, pb.b_hi.w};
+// One of the lane's two channel runs: 16 values from four dwords of sm, code and base bytes
+// (codes in the low nibbles for the run 16g.., high nibbles for 64+16g..).
+template <bool Z, bool HIGH>
+__device__ inline void rebuild_run(const uint4& sm, const uint4& code, const uint4& base, uint32_t out[8]) {
+    const uint32_t S[4] = {sm.x, sm.y, sm.z, sm.w};
+    const uint32_t C[4] = {code.x, code.y, code.z, code.w};
+    const uint32_t B[4] = {base.x, base.y, base.z, base.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t cl = C[i] & 0x0F0F0F0Fu;
-        const uint32_t ch = (C[i] >> 4) & 0x0F0F0F0Fu;
-        if (Z) {
-            rebuild4<true>(S[i], cl, BL[i] & 0x7F7F7F7Fu, BL[i] & 0x80808080u, out[2 * i], out[2 * i + 1]);
-            rebuild4<true>(SH[i], ch, BH[i] & 0x7F7F7F7Fu, BH[i] & 0x80808080u, out[8 + 2 * i], out[8 + 2 * i + 1]);
-        } else {                               // no zero flag in the page: base bytes are < 128
-            rebuild4<false>(S[i], cl, BL[i], 0u, out[2 * i], out[2 * i + 1]);
-            rebuild4<false>(SH[i], ch, BH[i], 0u, out[8 + 2 * i], out[8 + 2 * i + 1]);
-        }
+        const uint32_t cn = (HIGH ? C[i] >> 4 : C[i]) & 0x0F0F0F0Fu;
+        rebuild4<Z>(S[i], cn, B[i], out[2 * i], out[2 * i + 1]);
     }
 }
 
-// Rebuild the lane's 32 values (the zero-group fix-up only when a group of this page
-// carries the zero flag, decided for the whole wavefront).
+// Rebuild the lane's 32 values. The zero-group fix-up runs per channel run (channels 0-63
+// and 64-127 of the page) and only when some group of that run carries the zero flag,
+// decided for the whole wavefront (a page flags a run far less often than it flags one of
+// its two runs).
 __device__ inline void rebuild_values(const PageBytes& pb, uint32_t out[16]) {
-    const uint32_t fl = (pb.b_lo.x | pb.b_lo.y | pb.b_lo.z | pb.b_lo.w | pb.b_hi.x | pb.b_hi.y |
-                         pb.b_hi.z | pb.b_hi.w) & 0x80808080u;
-    if (__ballot(fl != 0) != 0) {             // any zero-flagged group in this page
-        rebuild_page_impl<true>(pb, out);
-    } else {
-        rebuild_page_impl<false>(pb, out);
-    }
+    const uint32_t flo = (pb.b_lo.x | pb.b_lo.y | pb.b_lo.z | pb.b_lo.w) & 0x80808080u;
+    const uint32_t fhi = (pb.b_hi.x | pb.b_hi.y | pb.b_hi.z | pb.b_hi.w) & 0x80808080u;
+    if (__ballot(flo != 0) != 0)
+        rebuild_run<true, false>(pb.sm_lo, pb.code, pb.b_lo, out);
+    else
+        rebuild_run<false, false>(pb.sm_lo, pb.code, pb.b_lo, out);
+    if (__ballot(fhi != 0) != 0)
+        rebuild_run<true, true>(pb.sm_hi, pb.code, pb.b_hi, out + 8);
+    else
+        rebuild_run<false, true>(pb.sm_hi, pb.code, pb.b_hi, out + 8);
 }
 
 // Slot of token r's raw row: rowoff + popcount(rowmask & ((1 << r) - 1)) (reference

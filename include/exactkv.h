@@ -123,6 +123,14 @@ int exkv_cache_open_pages_paged(int32_t* rowmask, int32_t* rowoff, const int32_t
                                 int32_t max_pages, int32_t pool_pages, int64_t cap, int64_t raw_rows, int32_t H,
                                 hipStream_t stream);
 
+/* Timing hook: the next split-kernel launch on the calling thread (any exkv_attn_* entry
+ * point) records `start` and `stop` (hipEvent_t, created by the caller; either may be NULL)
+ * at its own start and end, so a benchmark reads that kernel's duration from HIP events on
+ * the launch stream. One launch consumes the pair. No counterpart in the reference (its
+ * benchmark times whole calls with triton.testing.do_bench, bench/attention.py:72-78). */
+typedef struct ihipEvent_t* hipEvent_t;
+int exkv_time_next_split(hipEvent_t start, hipEvent_t stop);
+
 /* Wire form of a sequence's compressed cache: one contiguous little-endian blob
  *   header  256 B: u32 magic 0x564B5845 ("EXKV"), version 1, heads H, head_dim 128,
  *           tokens T, full_pages T/16, tail_rows T%16, raw_rows N; u64 off_tail,

@@ -1,5 +1,5 @@
 // Exhaustive CPU check of the 4-channel value rebuild used by the HIP decoder
-// (exactkv_amd/csrc/common.hpp rebuild4) against the scalar format rule
+// (exactkv_amd/csrc/common.hpp rebuild4, exponents) against the scalar format rule
 // (reference exactkv/codec.py:65-68): for every sign|mantissa byte, every base byte and
 // every 4-bit code, in every byte lane, with random neighbours in the other lanes.
 #include "../../exactkv_amd/csrc/common.hpp"
@@ -23,13 +23,13 @@ int main() {
                     uint32_t s[4], c[4], b[4];
                     for (int i = 0; i < 4; ++i) { s[i] = next() & 255; c[i] = next() & 15; b[i] = next() & 255; }
                     s[lane] = sm; c[lane] = code; b[lane] = base;
-                    uint32_t S = 0, CN = 0, BM = 0, ZF = 0;
+                    uint32_t S = 0, CN = 0, BB = 0, ZF = 0;
                     for (int i = 0; i < 4; ++i) {
                         S |= s[i] << (8 * i); CN |= c[i] << (8 * i);
-                        BM |= (b[i] & 127) << (8 * i); ZF |= (b[i] & 128) << (8 * i);
+                        BB |= b[i] << (8 * i); ZF |= (b[i] & 128) << (8 * i);
                     }
                     uint32_t o01, o23, p01, p23;
-                    exkv::rebuild4<true>(S, CN, BM, ZF, o01, o23);
+                    exkv::rebuild4<true>(S, CN, BB, o01, o23);
                     uint16_t got[4] = {(uint16_t)o01, (uint16_t)(o01 >> 16), (uint16_t)o23, (uint16_t)(o23 >> 16)};
                     for (int i = 0; i < 4; ++i) {
                         ++n;
@@ -37,7 +37,7 @@ int main() {
                     }
                     // without zero groups the fast variant must agree whenever no flag is set
                     if (ZF == 0) {
-                        exkv::rebuild4<false>(S, CN, BM, ZF, p01, p23);
+                        exkv::rebuild4<false>(S, CN, BB, p01, p23);
                         if (p01 != o01 || p23 != o23) { ++bad; }
                     }
                 }

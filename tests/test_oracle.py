@@ -312,3 +312,36 @@ def test_bits_per_value_closed_form(golden, name):
         assert N == 0 and bits_per_value(c) == 12.53125
     if name == "allpat_identity":
         assert N > 0 and bits_per_value(c) > 12.53125
+
+
+# ---------------------------------------------------------------- the torch CPU baseline
+
+@pytest.mark.parametrize("name", list(cases.CASES))
+def test_torch_codec_matches_reference_vectors(golden, name):
+    """oracle.torch_codec (the timed CPU baseline) writes the reference codec's bytes and
+    decodes them back exactly."""
+    from oracle import torch_codec
+    z, h = golden
+    make, stored = cases.CASES[name]
+    x = make()
+    c = torch_codec.encode(x)
+    for k in FIELDS:
+        a = c[k].contiguous().view(torch.int16).numpy().view(np.uint16) if k == "raw" else c[k].numpy()
+        if stored:
+            assert np.array_equal(a, z[f"{name}/{k}"]), (name, k)
+        else:
+            assert _sha(a) == h["cases"][name][k]["sha256"], (name, k)
+    assert torch.equal(torch_codec.decode(c).view(torch.int16), x.view(torch.int16)), name
+
+
+def test_torch_attention_matches_the_oracle():
+    from oracle import torch_codec
+    g = torch.Generator().manual_seed(11)
+    B, T, Hq, Hkv = 2, 77, 12, 3
+    q = torch.randn(B, Hq, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, 80, Hkv, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, 80, Hkv, 128, generator=g).to(torch.bfloat16)
+    lens = [77, 40]
+    got = torch_codec.attention(q, k, v, T, lens=lens).numpy()
+    want = oatt.attention(u16(q), u16(k), u16(v), T, np.float64, lens=lens)
+    assert np.abs(got - want).max() < 1e-5

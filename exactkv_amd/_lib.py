@@ -52,6 +52,9 @@ SIGNATURES = {
                          _i32, _i32, _p, _i64, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
     "exkv_time_next_split": [_p, _p],
+    "exkv_attn_compressed_noalloc": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32,
+                                     _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
+    "exkv_noalloc_scratch_bytes": [],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],
     "exkv_last_error": [],
@@ -77,7 +80,8 @@ def load():
     for name, args in SIGNATURES.items():
         f = getattr(lib, name)
         f.argtypes = args
-        f.restype = {"exkv_last_error": ctypes.c_char_p, "exkv_wire_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
+        f.restype = {"exkv_last_error": ctypes.c_char_p, "exkv_wire_bytes": ctypes.c_int64,
+                     "exkv_noalloc_scratch_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
     v = lib.exkv_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libexactkv_hip.so ABI version {v}, expected {ABI_VERSION}: rebuild the library")

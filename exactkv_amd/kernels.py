@@ -195,6 +195,28 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     return out
 
 
+def attention_compressed_noalloc(q, kc, vc, T, *, out, lens=None, nsplit=None, split_len=None, window=0):
+    """attention_compressed for callers that cannot allocate device memory (HIP-graph capture,
+    serving loops): the caller passes `out`, and the split partials go to the library's fixed
+    per-GPU scratch array (exkv_attn_compressed_noalloc) instead of a workspace. Contiguous
+    caches only. Calls that overlap on one GPU share that array and race; a plan with more
+    than the scratch's B * Hq * nsplit partials raises."""
+    _check_q(q)
+    if out is None or out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    ka, TS, Hkv, Bc = _cache_args(kc)
+    va, TSv, Hv, Bv = _cache_args(vc)
+    B, Hq, D = q.shape
+    if (TSv, Hv) != (TS, Hkv) or Bc < B or Bv < B:
+        raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
+    window = _window_arg(window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
+    lp, lstride = _lens_arg(lens, B)
+    _lib.call("exkv_attn_compressed_noalloc", _lib.ptr(q), *ka, *va, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp,
+              lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream(q.device.index))
+    return out
+
+
 def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
                         split_len=None, out=None, fused_merge=False, block_table=None, window=0):
     """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous);

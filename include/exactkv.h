@@ -214,6 +214,26 @@ int exkv_attn_compressed(const void* q, const void* k_sm, const void* k_code, co
                          const int32_t* lens, int64_t lens_stride, int32_t nsplit, int32_t split_len,
                          int32_t window, float qk_scale, hipStream_t stream);
 
+/* exkv_attn_compressed with no workspace argument and no allocation, for callers that cannot
+ * allocate (code under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The split partials go to a fixed scratch
+ * array in device memory that the library holds on every GPU it runs on, for the life of
+ * the process: at most exkv_noalloc_scratch_bytes() (32 MiB) = B * Hq * nsplit * 130 * 4
+ * bytes, so B * Hq * nsplit <= 64,527; larger calls return 1 with a message. The merge runs
+ * as the second kernel. Call with the stream's device current. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams or threads) race. Same
+ * arguments otherwise, and the same bits as exkv_attn_compressed. */
+int exkv_attn_compressed_noalloc(const void* q, const void* k_sm, const void* k_code, const void* k_base,
+                                 const int32_t* k_rowmask, const int32_t* k_rowoff, const void* k_raw,
+                                 int64_t k_raw_rows, const void* v_sm, const void* v_code, const void* v_base,
+                                 const int32_t* v_rowmask, const int32_t* v_rowoff, const void* v_raw,
+                                 int64_t v_raw_rows, void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                                 int32_t T, int32_t TS, const int32_t* lens, int64_t lens_stride, int32_t nsplit,
+                                 int32_t split_len, int32_t window, float qk_scale, hipStream_t stream);
+
+/* Size in bytes of exkv_attn_compressed_noalloc's per-GPU scratch array. */
+int64_t exkv_noalloc_scratch_bytes(void);
+
 /* The same attention over plain bf16 caches k, v [B, TS, Hkv, 128].
  * Replaces: kernels.py:321-328 attention_reference (_split_ref_kernel :168-194). */
 int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,

@@ -52,6 +52,7 @@ SIGNATURES = {
                          _i32, _i32, _p, _i64, _p],
     "exkv_attn_reduce": [_p, _p, _p, _p, _i64, _i32, _i32, _p],
     "exkv_time_next_split": [_p, _p],
+    "exkv_merge_counters": [_i32, _i32, _i32, _i32],
     "exkv_attn_compressed_noalloc": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_noalloc_scratch_bytes": [],
@@ -81,7 +82,8 @@ def load():
         f = getattr(lib, name)
         f.argtypes = args
         f.restype = {"exkv_last_error": ctypes.c_char_p, "exkv_wire_bytes": ctypes.c_int64,
-                     "exkv_noalloc_scratch_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
+                     "exkv_noalloc_scratch_bytes": ctypes.c_int64,
+                     "exkv_merge_counters": ctypes.c_int64}.get(name, ctypes.c_int)
     v = lib.exkv_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libexactkv_hip.so ABI version {v}, expected {ABI_VERSION}: rebuild the library")

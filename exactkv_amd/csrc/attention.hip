@@ -46,7 +46,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kFusedMaxSplits = 4;   // up to this many splits the split kernel merges in its tail
+constexpr int kFusedMaxSplits = 1024;   // up to this many splits the split kernel can merge in its tail
 constexpr int kDmaPerPage[2] = {8, 8}; // direct-to-LDS loads per page: bf16, compressed (raw row included)
 
 // compressed page stage (bytes): K sm 16x128 | K code 16x64 | V sm | V code | K base,
@@ -476,26 +476,119 @@ __device__ inline void write_v_tile(uint32_t sb, const LdsLane& o, int toff, con
     lds_st16(p + 144, v[12], v[13], v[14], v[15]);
 }
 
-// After a workgroup has written its partials: count it in; the last workgroup of the unit
-// (sequence b, head block hb, head group hg) merges all splits of its query heads.
+// ---- the merge in the split kernel's tail (counters != nullptr)
+//
+// Partials are written with device-scope stores, which go through the L2 of the writer's
+// XCD to memory, and read with device-scope loads; a workgroup counts itself in only once
+// its own stores are complete (s_waitcnt vmcnt(0) before the counter's atomic add). So the
+// last workgroup of a group sees every partial of the group without an L2 write-back or
+// invalidate (a device-scope release / acquire, which on a multi-XCD part writes back the
+// XCD's whole L2: measured slower than a second kernel at every grid size).
+//
+// Two levels keep each merge short: the splits of a unit form groups of merge_group(ns)
+// consecutive splits; the last workgroup to finish a group merges it into the group's first
+// split slot (un-normalised o, max m, sum l), and the last group merger of the unit merges
+// the groups into the output. Counters: [unit][group] then [unit][ngroups] for the second
+// level, all zero between calls (each merger resets the one it consumed).
+__device__ inline void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float ld_dev(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline void st_dev4(float* p, const f32x4& v) {
+    st_dev(p, v[0]);
+    st_dev(p + 1, v[1]);
+    st_dev(p + 2, v[2]);
+    st_dev(p + 3, v[3]);
+}
+
+__host__ __device__ inline int merge_group(int ns) {
+    if (ns <= 8) return ns;                            // one level (the separate merge's bits)
+    int g = 1;
+    while (g * g < ns) ++g;                            // ceil(sqrt(ns)): both levels about as long
+    return g;
+}
+__host__ __device__ inline int merge_groups(int ns) { return (ns + merge_group(ns) - 1) / merge_group(ns); }
+
+// One row (sequence, query head): merge splits s0, s0 + step, ... (n <= 32 of them, all
+// loads in flight together), lane = channel pair. Returns the un-normalised sums and the
+// common maximum; a row whose splits are all empty gives m = -inf, l = 0, o = 0.
+struct RowMerge {
+    float n0, n1, den, M;
+};
+__device__ inline RowMerge merge_row_dev(const AttnArgs& a, int64_t row, int s0, int step, int n, int lane) {
+    const float* po = a.part_o + row * a.nsplit * kD;
+    const float* pm = a.part_m + row * a.nsplit;
+    const float* pl = a.part_l + row * a.nsplit;
+    const float mv = lane < n ? ld_dev(pm + s0 + lane * step) : -INFINITY;
+    const float lv = lane < n ? ld_dev(pl + s0 + lane * step) : 0.f;
+    float ox[32], oy[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        if (i < n) {
+            const float* p = po + (int64_t)(s0 + i * step) * kD + 2 * lane;
+            ox[i] = ld_dev(p);
+            oy[i] = ld_dev(p + 1);
+        }
+    const float M = wave_max(mv);
+    const float ws = M == -INFINITY ? 0.f : fast_exp2(mv - M);
+    RowMerge r{0.f, 0.f, 0.f, M};
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        if (i < n) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), i));
+            const float li = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), i));
+            r.n0 = __builtin_fmaf(ox[i], w, r.n0);
+            r.n1 = __builtin_fmaf(oy[i], w, r.n1);
+            r.den = __builtin_fmaf(li, w, r.den);
+        }
+    return r;
+}
+
+// Count this workgroup in at counter c (after every wave's stores are complete); true for
+// the workgroup that completes a count of n, which also resets the counter.
+__device__ inline bool arrive_last(int32_t* c, int n) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == n - 1;
+        if (old == n - 1) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return s_last != 0;
+}
+
+// After a workgroup has written its partials (rows of heads hb*HW .. of sequence b, query
+// group hg, split `split`): the two-level merge above.
 __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int gh, int split) {
     if (a.counters == nullptr) return;
-    __shared__ int s_last;
-    __threadfence();                                   // release this workgroup's partials
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&a.counters[blockIdx.y], 1) == a.nsplit - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();                                   // acquire the other workgroups' partials
+    const int G1 = merge_group(a.nsplit), ng = merge_groups(a.nsplit);
+    const int grp = split / G1, g0 = grp * G1, gn = min(G1, a.nsplit - g0);
+    int32_t* cnt = a.counters + (int64_t)blockIdx.y * (ng + 1);
+    if (!arrive_last(cnt + grp, gn)) return;
     const int rows = a.HW * gh, lane = threadIdx.x & 63;
-    for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {   // wavefront per row, lane = channel pair
-        const int h = i % gh, hs = i / gh;
-        const int64_t row = (int64_t)b * a.Hq + (int64_t)(hb * a.HW + hs) * a.G + hg * 16 + h;
-        reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] = merge_direct<kFusedMaxSplits>(
-            a.part_o + row * a.nsplit * kD, a.part_m + row * a.nsplit, a.part_l + row * a.nsplit, a.nsplit, lane);
+    auto row_of = [&](int i) {
+        return (int64_t)b * a.Hq + (int64_t)(hb * a.HW + i / gh) * a.G + hg * 16 + i % gh;
+    };
+    if (ng > 1) {                                      // level 1: the group into its first split slot
+        for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {
+            const int64_t row = row_of(i);
+            const RowMerge r = merge_row_dev(a, row, g0, 1, gn, lane);
+            float* po = a.part_o + (row * a.nsplit + g0) * kD + 2 * lane;
+            st_dev(po, r.n0);
+            st_dev(po + 1, r.n1);
+            if (lane == 0) {
+                st_dev(a.part_m + row * a.nsplit + g0, r.M);
+                st_dev(a.part_l + row * a.nsplit + g0, r.den);
+            }
+        }
+        if (!arrive_last(cnt + ng, ng)) return;
     }
-    if (threadIdx.x == 0) a.counters[blockIdx.y] = 0;  // ready for the next call on this workspace
-    (void)split;
+    const int step = ng > 1 ? G1 : 1, n2 = ng > 1 ? ng : a.nsplit;
+    for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {    // level 2: the groups (or splits) into the output
+        const int64_t row = row_of(i);
+        const RowMerge r = merge_row_dev(a, row, 0, step, n2, lane);
+        reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] = pack_bf16x2(r.n0 / r.den, r.n1 / r.den);
+    }
 }
 
 template <bool COMP>
@@ -824,12 +917,21 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     if (nphase == 1) {                                 // one wavefront per head: write its partial
         if (r < gh) {
             const int64_t prow = (hq0 + r) * a.nsplit + split;
+            if (a.counters == nullptr) {
 #pragma unroll
-            for (int nb = 0; nb < 8; ++nb)
-                *reinterpret_cast<f32x4*>(a.part_o + prow * kD + 16 * nb + 4 * g) = acc[nb];
-            if (g == 0) {
-                a.part_m[prow] = m_i;
-                a.part_l[prow] = l_t;
+                for (int nb = 0; nb < 8; ++nb)
+                    *reinterpret_cast<f32x4*>(a.part_o + prow * kD + 16 * nb + 4 * g) = acc[nb];
+                if (g == 0) {
+                    a.part_m[prow] = m_i;
+                    a.part_l[prow] = l_t;
+                }
+            } else {                                   // merged in this kernel: device-scope stores
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) st_dev4(a.part_o + prow * kD + 16 * nb + 4 * g, acc[nb]);
+                if (g == 0) {
+                    st_dev(a.part_m + prow, m_i);
+                    st_dev(a.part_l + prow, l_t);
+                }
             }
         }
         merge_tail(a, b, hb, hg, gh, split);
@@ -864,10 +966,18 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
         }
         const int64_t prow = ((int64_t)b * a.Hq + (int64_t)(hb * a.HW + hs) * a.G + hg * 16 + h) * a.nsplit + split;
-        a.part_o[prow * kD + d] = o;
-        if (d == 0) {
-            a.part_m[prow] = M;
-            a.part_l[prow] = l;
+        if (a.counters == nullptr) {
+            a.part_o[prow * kD + d] = o;
+            if (d == 0) {
+                a.part_m[prow] = M;
+                a.part_l[prow] = l;
+            }
+        } else {
+            st_dev(a.part_o + prow * kD + d, o);
+            if (d == 0) {
+                st_dev(a.part_m + prow, M);
+                st_dev(a.part_l + prow, l);
+            }
         }
     }
     merge_tail(a, b, hb, hg, gh, split);
@@ -974,6 +1084,12 @@ static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kThreads), 0, stream, a);
     }
     return hip_status(hipGetLastError(), comp ? "attn_split_compressed" : "attn_split_bf16");
+}
+
+extern "C" int64_t exkv_merge_counters(int32_t B, int32_t Hq, int32_t Hkv, int32_t nsplit) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || nsplit <= 0 || nsplit > kFusedMaxSplits) return -1;
+    const int64_t units = (int64_t)B * (Hkv / heads_per_block(Hkv)) * ((Hq / Hkv + 15) / 16);
+    return units * (merge_groups(nsplit) + 1);
 }
 
 extern "C" int exkv_time_next_split(hipEvent_t start, hipEvent_t stop) {

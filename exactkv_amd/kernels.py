@@ -65,26 +65,33 @@ def merge_units(B, Hkv, Hq):
     return B * (Hkv // math.gcd(Hkv, 8)) * (-(-(Hq // Hkv) // 16))
 
 
-FUSED_MERGE_MAX_SPLITS = 4   # up to this many splits the split kernel's last workgroup can merge
-# The fused merge is available (fused_merge=True) but not the default: every workgroup's
-# device-scope release writes back its XCD's L2, and measured on MI355X that costs more
-# than the separate merge launch at every grid size tried (16 workgroups: +5 us, 64: +14 us,
-# 256: +78 us per call).
+FUSED_MERGE_MAX_SPLITS = 1024   # up to this many splits the split kernel can merge in its tail
+# With fused_merge the split kernel's last workgroups merge the partials (two levels of
+# about sqrt(nsplit) splits each; one level up to 8 splits, with the separate merge's
+# bits), writing them with device-scope stores so that no L2 write-back is needed.
+# It is not the default: measured on MI355X under graph replay it costs more than the
+# separate merge launch (c2a 62.6 vs 47.1 us per call, c2b 101.7 vs 85.1, c1 41.7 vs 27.9):
+# every workgroup waits for its stores and an arrival atomic before it can retire, which
+# delays the workgroups queued behind it, while the separate merge adds 1.5 us at c2a.
 
 
-def _counters(dev, units):
-    key = (dev.index, _lib.stream(), units)
+def _counters(dev, n):
+    key = (dev.index, _lib.stream(), n)
     c = _CNT.get(key)
     if c is None:
-        c = _CNT[key] = torch.zeros(units, dtype=torch.int32, device=dev)
+        c = _CNT[key] = torch.zeros(n, dtype=torch.int32, device=dev)
     return c
 
 
 def _fused_counters(dev, B, Hkv, Hq, ns, fused_merge):
-    """Arrival counters when the merge runs in the split kernel's tail, else None."""
+    """Arrival counters (zero between calls) when the merge runs in the split kernel's tail,
+    else None."""
     if not fused_merge or ns > FUSED_MERGE_MAX_SPLITS:
         return None
-    return _counters(dev, merge_units(B, Hkv, Hq))
+    n = _lib.load().exkv_merge_counters(B, Hq, Hkv, ns)
+    if n < 0:
+        raise ValueError(f"no fused merge for B={B} Hq={Hq} Hkv={Hkv} nsplit={ns}")
+    return _counters(dev, n)
 
 
 def _check_q(q):

@@ -123,6 +123,11 @@ int exkv_cache_open_pages_paged(int32_t* rowmask, int32_t* rowoff, const int32_t
                                 int32_t max_pages, int32_t pool_pages, int64_t cap, int64_t raw_rows, int32_t H,
                                 hipStream_t stream);
 
+/* Number of int32 arrival counters ws_cnt must hold for the merge in the split kernel's tail
+ * (units x (groups + 1)), or -1 for arguments with no fused merge (nsplit > 1024).
+ * Replaces: the workspace sizing of kernels.py:280-290 (_WS), for the counters. */
+int64_t exkv_merge_counters(int32_t B, int32_t Hq, int32_t Hkv, int32_t nsplit);
+
 /* Timing hook: the next split-kernel launch on the calling thread (any exkv_attn_* entry
  * point) records `start` and `stop` (hipEvent_t, created by the caller; either may be NULL)
  * at its own start and end, so a benchmark reads that kernel's duration from HIP events on
@@ -191,11 +196,12 @@ int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base
 
 /* Split-K GQA decode attention over compressed K and V caches, then the split merge.
  * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
- * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: B*(Hkv/gcd(Hkv,8))*ceil(Hq/Hkv/16) i32 arrival
- * counters, all zero before the first call (each call leaves them zero); with ws_cnt and
- * nsplit <= 4 the merge runs inside the split kernel (its last workgroup per unit),
- * otherwise as a second kernel (same bits; ws_cnt may be NULL). Calls that share a
- * workspace must not overlap.
+ * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: exkv_merge_counters(B, Hq, Hkv, nsplit) i32
+ * arrival counters, all zero before the first call (each call leaves them zero). With
+ * ws_cnt (and nsplit <= 1024) the merge runs inside the split kernel: the last workgroups
+ * of each unit merge groups of about sqrt(nsplit) splits, then the groups (one level, with
+ * the separate merge's bits, up to 8 splits); without it, as a second kernel. Calls that
+ * share a workspace must not overlap.
  * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
  * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
  * window > 0 (sliding-window attention): only the last `window` of those tokens,

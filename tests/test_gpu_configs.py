@@ -49,17 +49,23 @@ def _data(B, TS, Hq, Hkv, seed, raw_row_rate=3e-3):
 
 
 def _check_call(q, k, v, kc, vc, kd, vd, T, lens=None, fp64=True, **kw):
-    """compressed == twin bitwise; fp32-oracle tolerance; the fp64 bound of the reference test."""
+    """compressed == twin bitwise, with the merge as a second kernel and in the split kernel's
+    tail; fp32-oracle tolerance for both; the fp64 bound of the reference test."""
     qd = q.to(DEV)
     ld = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=DEV)
     o_c = kernels.attention_compressed(qd, kc, vc, T, lens=ld, **kw)
     o_r = kernels.attention_reference(qd, kd, vd, T, lens=ld, **kw)
+    f_c = kernels.attention_compressed(qd, kc, vc, T, lens=ld, fused_merge=True, **kw)
+    f_r = kernels.attention_reference(qd, kd, vd, T, lens=ld, fused_merge=True, **kw)
     torch.cuda.synchronize()
     assert same_bits(o_c, o_r), "compressed and bf16 twin differ"
+    assert same_bits(f_c, f_r), "compressed and bf16 twin differ (merge in the split kernel)"
     assert torch.isfinite(o_c.float()).all()
     kq, vq = u16(k), u16(v)
     qq = u16(q)
-    assert_bf16_tolerance(o_c, oatt.attention(qq, kq, vq, T, np.float32, lens=lens))
+    r32 = oatt.attention(qq, kq, vq, T, np.float32, lens=lens)
+    assert_bf16_tolerance(o_c, r32)
+    assert_bf16_tolerance(f_c, r32)
     if fp64:
         r64 = oatt.attention(qq, kq, vq, T, np.float64, lens=lens)
         assert np.abs(o_c.double().cpu().numpy() - r64).max() < 2e-2
@@ -170,6 +176,11 @@ def test_long_splits_walk_past_64_pages(paged):
     assert same_bits(o_p, o_pb)
     assert same_bits(o_p, o_g)
     assert_bf16_tolerance(o_p, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+    # the default plan through the block table, merged in the split kernel's tail
+    f_p = kernels.attention_compressed(qd, kpc, vpc, T, block_table=bt, fused_merge=True)
+    assert same_bits(f_p, kernels.attention_reference(qd, kpd, vpd, T, block_table=bt, fused_merge=True))
+    assert same_bits(f_p, kernels.attention_reference(qd, kd, vd, T, fused_merge=True))
+    assert_bf16_tolerance(f_p, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
 
 
 def test_c3_qwen3_b32_variable_lengths_growth_and_appends():
@@ -209,8 +220,11 @@ def test_c3_qwen3_b32_variable_lengths_growth_and_appends():
             ld = torch.tensor(lens, dtype=torch.int32, device=DEV)
             o_c = kernels.attention_compressed(qd, kc, vc, T, lens=ld)
             assert same_bits(o_c, kernels.attention_reference(qd, kr.buf, vr.buf, T, lens=ld)), T
+            f_c = kernels.attention_compressed(qd, kc, vc, T, lens=ld, fused_merge=True)
+            assert same_bits(f_c, kernels.attention_reference(qd, kr.buf, vr.buf, T, lens=ld, fused_merge=True)), T
             ref = oatt.attention(u16(q), u16(k[:, :T]), u16(v[:, :T]), T, np.float32, lens=lens)
             assert oatt.tolerance_excess(o_c.float().cpu().numpy(), ref) <= 0, T
+            assert oatt.tolerance_excess(f_c.float().cpu().numpy(), ref) <= 0, T
             assert same_bits(exactkv.decode_attention(qd, kc, vc), exactkv.decode_attention(qd, kr, vr)), T
             checked += 1
     assert checked >= 5

@@ -10,8 +10,9 @@ The Infinity Cache (256 MB) is defeated by rotating over several cache copies.
 Prints one JSON line: value = microseconds per call (lower is better), the roofline of the
 dominant kernel (the split kernel: algorithmic bytes / its average duration, HIP events on
 the launch stream), the bf16-uncompressed twin for comparison, the encoder's throughput,
-and the CPU baseline (the oracle codec decode + fp32 attention on the host, one thread,
-on a sample of the sequences, scaled to the full call).
+and the CPU baseline (the reference codec restated in PyTorch decoding both caches, then
+fp32 attention, on every host core this process may use; median of full calls).
+--workload cpu times that baseline at every benchmark shape without the GPU.
 
     python bench.py [--steps 50] [--warmup 10] [--workload c2a]
 """
@@ -235,7 +236,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2a",
-                    choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill", "e2e_paged"])
+                    choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
@@ -251,12 +252,12 @@ def main():
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel; no timing")
     a = ap.parse_args()
-    if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged"):
+    if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
         return {"e2e": e2e, "c3": c3_stress, "c2a_paged": paged_c2a, "wire": wire_bench,
-                "prefill": prefill_bench, "e2e_paged": e2e_paged}[a.workload](a)
+                "prefill": prefill_bench, "e2e_paged": e2e_paged, "cpu": cpu_sweep}[a.workload](a)
     if a.profile:
         a.copies = 1
     if a.gpus != 1:
@@ -596,6 +597,73 @@ def c3_stress(a):
         "bit_identical_to_bf16": bool(identical), "pool_grows_in_prefill": grows[0],
         "raw_rows": int(kcs[0].cnt.item()) + int(vcs[0].cnt.item()), "encoder_GBps": enc,
         "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(res), flush=True)
+
+
+def cpu_sweep(a):
+    """The CPU baseline at every benchmark shape, on the host cores only (no GPU work): the
+    reference codec restated in PyTorch (oracle.torch_codec, byte-identical to codec.py) and
+    fp32 GQA attention, with torch using every core this process may run on. Each figure is
+    the median of --cpu-runs timed runs (time.perf_counter):
+      encode GB/s   config 0's keys (1 x 4096 x 4 heads) and the c3 prefill (32 x 4096 x 8
+                    heads, keys, 0.6% outlier rows): (bf16 read + compressed written) / time;
+      decode GB/s   the c3 prefill's keys back to bf16: (compressed read + bf16 written) / time;
+      attention ms  c1, c2a, c2b and c3 (per-sequence lengths): decode K and V, then attention,
+                    on the same seeded data as the GPU benchmark of that shape."""
+    import numpy as np
+    import torch
+    from exactkv_amd import synthetic
+    from oracle import torch_codec
+
+    n = cpu_threads()
+    torch.set_num_threads(n)
+    runs = a.cpu_runs
+
+    def comp_bytes(c):
+        return sum(c[f].numel() * c[f].element_size() for f in ("sm", "code", "base", "rowmask", "rowoff", "raw"))
+
+    def log(msg):
+        print(f"[cpu] {msg}", file=sys.stderr, flush=True)
+
+    enc, dec, attn = {}, {}, {}
+    for name, (B, T, H, kw) in {"c0": (1, 4096, 4, {}), "c3": (32, 4096, 8, {"raw_row_rate": 6e-3})}.items():
+        x = synthetic.make_kv(B, T, H, kind="k", seed=100, **kw)
+        c = torch_codec.encode(x)
+        t, _ = median_seconds(lambda: torch_codec.encode(x), runs)
+        enc[name] = {"GBps": round((x.numel() * 2 + comp_bytes(c)) / t / 1e9, 3), "s": round(t, 4),
+                     "shape": [B, T, H, 128]}
+        log(f"encode {name}: {enc[name]}")
+        if name == "c3":
+            t, _ = median_seconds(lambda: torch_codec.decode(c), runs)
+            dec[name] = {"GBps": round((x.numel() * 2 + comp_bytes(c)) / t / 1e9, 3), "s": round(t, 4),
+                         "shape": [B, T, H, 128]}
+            log(f"decode {name}: {dec[name]}")
+        del x, c
+    shapes = {"c1": (1, 32768, 28, 4, 3e-3, None), "c2a": (8, 8192, 32, 8, 3e-3, None),
+              "c2b": (1, 131072, 32, 8, 3e-3, None), "c3": (32, 4096, 32, 8, 6e-3, 300)}
+    for name, (B, T, Hq, Hkv, rate, lseed) in shapes.items():
+        k = synthetic.make_kv(B, T, Hkv, kind="k", seed=100, raw_row_rate=rate)
+        v = synthetic.make_kv(B, T, Hkv, kind="v", seed=101, raw_row_rate=rate)
+        q = synthetic.make_q(B, Hq, seed=102)
+        lens = None if lseed is None else np.random.Generator(np.random.PCG64(lseed)).integers(3500, T + 1, B)
+        kc, vc = torch_codec.encode(k), torch_codec.encode(v)
+        del k, v
+        t, best = median_seconds(lambda: torch_codec.decode_attention(q, kc, vc, T, lens=lens), runs)
+        attn[name] = {"ms": round(t * 1e3, 2), "min_ms": round(best * 1e3, 2), "B": B, "T": T, "Hq": Hq, "Hkv": Hkv,
+                      **({"lens": "U[3500, 4096] (PCG64 seed 300)"} if lens is not None else {})}
+        log(f"attention {name}: {attn[name]}")
+        del kc, vc
+    res = {
+        "metric": "CPU baseline: torch restatement of the reference codec + fp32 attention on the host cores",
+        "value": attn["c2a"]["ms"], "unit": "ms", "n_gpus": 0, "steps": runs, "warmup": 0,
+        "ms_per_step": attn["c2a"]["ms"], "higher_is_better": False, "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "cpu: encode c0 / c3 prefill, decode c3 prefill, decode+attention c1 / c2a / c2b / c3",
+                   "runs": runs},
+        "encode": enc, "decode": dec, "attention": attn,
+        "cores": n, "torch_threads": torch.get_num_threads(), "cpu": cpu_model(),
+        "timing": f"time.perf_counter, median of {runs} runs each",
     }
     print(json.dumps(res), flush=True)
 

@@ -72,16 +72,24 @@ __host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t base,
 
 __device__ inline int popc32(uint32_t x) { return __builtin_popcount(x); }
 
-// Block-wide exclusive scan of one int per thread (1024 threads).
+// Inclusive prefix sum across the 64 lanes of a wavefront (DPP row shifts within each row
+// of 16 lanes, then the row-15 and row-31 broadcasts into the rows above them).
+__device__ inline int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
+// Block-wide exclusive scan of one int per thread (1024 threads, all of them calling).
+// Synchronises on entry to the cross-wavefront step and before returning.
 __device__ inline int block_excl_scan(int v, int& total) {
     __shared__ int wsum[16];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(inc, off);
-        if (lane >= off) inc += y;
-    }
+    const int inc = wave_incl_scan(v);
     if (lane == 63) wsum[w] = inc;
     __syncthreads();
     int wpre = 0;

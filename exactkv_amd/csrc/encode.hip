@@ -29,7 +29,8 @@ __device__ inline uint8_t sm_byte(uint32_t u) { return (uint8_t)(((u >> 8) & 0x8
 // src + p * s_p, except row 15 which comes from `last` when given; rows must be 4-byte
 // aligned (even element offsets: callers check). Destination rows of consecutive tokens
 // are `rs` rows apart (rs = H).
-__device__ void encode_page(const uint16_t* src, int64_t s_p, const uint16_t* last, int lane,
+__device__ __attribute__((always_inline)) inline void encode_page(const uint16_t* src, int64_t s_p,
+                                                                  const uint16_t* last, int lane,
                             uint8_t* sm0, uint8_t* code0, int64_t rs, uint8_t* basep, int32_t* rmaskp) {
     const int half = lane >> 5, m = lane & 31;
     uint32_t lo[8], hi[8];                             // bf16 pairs: channels (2m, 2m+1), (2m+64, 2m+65)
@@ -154,57 +155,31 @@ __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunit
                 a.rowmask + page);
 }
 
-// Units u0 .. u1-1 of one scan thread, walked in order: coordinates by increment (one
-// division per thread), page indices and masks 8 at a time with every load of a group
-// issued before the first is used (clamped, no branch).
-struct UnitWalk {
-    int bi, pg, hk;
-    __device__ void next(const EncArgs& a) {
-        if (++hk == a.H) {
-            hk = 0;
-            if (++pg == a.npg) {
-                pg = 0;
-                ++bi;
-            }
-        }
-    }
-};
-
-__device__ inline void unit_group8(const EncArgs& a, UnitWalk& w, int64_t c, int64_t u1, int64_t page[8],
-                                   int n[8]) {
-    int bi[8], pg[8], hk[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        bi[k] = w.bi;
-        pg[k] = w.pg;
-        hk[k] = w.hk;
-        if (c + k + 1 < u1) w.next(a);                 // stays on the last unit past the end
-    }
-    if (a.dst_pages == nullptr) {                      // uniform
-#pragma unroll
-        for (int k = 0; k < 8; ++k) page[k] = ((int64_t)(a.b0 + bi[k]) * (a.TS / kPage) + (a.pg0 + pg[k])) * a.H + hk[k];
-    } else {
-        int32_t e[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = a.dst_pages[bi[k] * a.dst_stride + pg[k]];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            page[k] = (int64_t)min((uint64_t)(uint32_t)e[k], (uint64_t)(a.all_pages - 1)) * a.H + hk[k];
-    }
-    uint32_t m[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) m[k] = (uint32_t)a.rowmask[page[k]];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) n[k] = c + k < u1 ? popc32(m[k]) : 0;
-}
-
-// The slot scan in three launches over blocks of kScanUnits units (1024 threads x 8):
+// The slot scan after a page encode, one unit per thread and 1024 units per block, every
+// access coalesced:
 //   scan_count_kernel   block g: its units' raw rows -> the rowoff slot of its first unit;
 //   scan_blocks_kernel  one workgroup: exclusive scan of the block totals from the
 //                       counter -> the same slots; the counter advances by the total;
-//   scan_write_kernel   block g: rowoff = its slot's offset + running count in unit order.
-// The block totals need no workspace: the slot of a block's first unit is rewritten last.
-constexpr int64_t kScanUnits = 1024 * 8;
+//   scan_write_kernel   block g: rowoff = its slot's offset + the block's exclusive scan,
+//                       then each wavefront copies the raw rows of its escaped units.
+// The block totals need no workspace: the slot of a block's first unit is read by that
+// block alone, and its final value (the block's offset + 0) is the one read.
+constexpr int kScanUnits = 1024;
+
+// Coordinates and page (in the arrays read as pages x heads) of unit u, with the layout
+// fixed at compile time (unit counts are below 2^31: the entry points check).
+template <bool PAGED>
+__device__ inline int64_t unit_page32(const EncArgs& a, int u, int& bi, int& pg, int& hk) {
+    const int q = u / a.H;
+    hk = u - q * a.H;
+    bi = q / a.npg;
+    pg = q - bi * a.npg;
+    if (PAGED) {
+        const int32_t e = a.dst_pages[(int64_t)bi * a.dst_stride + pg];
+        return (int64_t)min((uint64_t)(uint32_t)e, (uint64_t)(a.all_pages - 1)) * a.H + hk;
+    }
+    return ((int64_t)(a.b0 + bi) * (a.TS / kPage) + (a.pg0 + pg)) * a.H + hk;
+}
 
 __device__ inline int64_t first_page_of(const EncArgs& a, int64_t g) {
     int bi, pg, hk;
@@ -212,28 +187,14 @@ __device__ inline int64_t first_page_of(const EncArgs& a, int64_t g) {
     return unit_page(a, bi, pg, hk);
 }
 
-__device__ inline int block_units(const EncArgs& a, int64_t nunits, int64_t& u0, int64_t& u1, int64_t page[8],
-                                  int n[8]) {
-    const int64_t b0 = (int64_t)blockIdx.x * kScanUnits;
-    u0 = min(b0 + (int64_t)threadIdx.x * 8, nunits);
-    u1 = min(u0 + 8, nunits);
-    int local = 0;
-    if (u0 < u1) {
-        UnitWalk w{0, 0, 0};
-        unit_coords(a, u0, w.bi, w.pg, w.hk);
-        unit_group8(a, w, u0, u1, page, n);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) local += n[k];
-    }
-    return local;
-}
-
-__global__ void __launch_bounds__(1024) scan_count_kernel(EncArgs a, int64_t nunits) {
-    int64_t u0, u1, page[8];
-    int n[8];
-    const int local = block_units(a, nunits, u0, u1, page, n);
+template <bool PAGED>
+__global__ void __launch_bounds__(1024) scan_count_kernel(EncArgs a, int nunits) {
+    const int u = blockIdx.x * kScanUnits + threadIdx.x;
+    int bi, pg, hk;
+    uint32_t m = 0;
+    if (u < nunits) m = (uint32_t)a.rowmask[unit_page32<PAGED>(a, u, bi, pg, hk)];
     int total;
-    block_excl_scan(local, total);
+    block_excl_scan(popc32(m), total);
     if (threadIdx.x == 0) a.rowoff[first_page_of(a, blockIdx.x)] = total;
 }
 
@@ -257,27 +218,105 @@ __global__ void __launch_bounds__(1024) scan_blocks_kernel(EncArgs a, int64_t nb
     }
 }
 
-__global__ void __launch_bounds__(1024) scan_write_kernel(EncArgs a, int64_t nunits) {
-    __shared__ int s_base;
-    if (threadIdx.x == 0) s_base = a.rowoff[first_page_of(a, blockIdx.x)];
-    __syncthreads();                                   // read before the slot is rewritten
-    int64_t u0, u1, page[8];
-    int n[8];
-    const int local = block_units(a, nunits, u0, u1, page, n);
-    int total;
-    int run = s_base + block_excl_scan(local, total);
+// The raw rows of the escaped units among a wavefront's 64 (lane = unit: mask m, first slot
+// off, source row 0 at src). VEC16 (source rows 16-byte aligned): four units at a time, a
+// 16-lane group per unit, each lane moving 16 bytes of every row of its unit with all the
+// unit's loads in flight; else one unit at a time, 4 bytes of each row per lane. Slots at
+// or past cap are skipped (the host grows the pool and encodes again).
+template <bool VEC16>
+__device__ inline void copy_escaped_rows(const EncArgs& a, uint32_t m, int32_t off, const uint16_t* src,
+                                         int lane) {
+    uint64_t todo = __ballot(m != 0);
+    if (VEC16) {
+        const int g = lane >> 4, j = lane & 15;
+        while (todo != 0) {
+            int pick = -1;                             // group g takes the g-th unit left
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if (u0 + k < u1) a.rowoff[page[k]] = run;
-        run += n[k];
+            for (int i = 0; i < 4; ++i)
+                if (todo != 0) {
+                    if (i == g) pick = __builtin_ctzll(todo);
+                    todo &= todo - 1;
+                }
+            const int from = pick < 0 ? 0 : pick;
+            // every lane joins the shuffles (a shuffle from a lane outside the executing
+            // ones reads 0): the unit's mask, first slot and source row
+            const uint32_t mv = (uint32_t)__shfl((int)m, from);
+            const uint32_t mp = pick < 0 ? 0u : mv;
+            const int32_t op = __shfl(off, from);
+            const uint64_t sp = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(uintptr_t)src, from)) |
+                                ((uint64_t)(uint32_t)__shfl((int)(uint32_t)((uintptr_t)src >> 32), from) << 32);
+            const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + 8 * j;
+            const int nr = popc32(mp);
+            uint32_t t = mp;
+            uint4 r[kPage];
+#pragma unroll
+            for (int k = 0; k < kPage; ++k) {          // the k-th escaped row of the unit
+                const int p = t != 0u ? __builtin_ctz(t) : 0;
+                t &= t - 1u;
+                r[k] = k < nr ? *reinterpret_cast<const uint4*>(s + p * a.s_p) : uint4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int k = 0; k < kPage; ++k)
+                if (k < nr && (int64_t)op + k < a.cap)
+                    *reinterpret_cast<uint4*>(a.raw + ((int64_t)op + k) * 128 + 8 * j) = r[k];
+        }
+    } else {
+        while (todo != 0) {
+            const int l = __builtin_ctzll(todo);
+            todo &= todo - 1;
+            const uint32_t mp = (uint32_t)__builtin_amdgcn_readlane((int)m, l);
+            const int32_t op = __builtin_amdgcn_readlane(off, l);
+            const uint64_t sp = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uintptr_t)src, l) |
+                                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uintptr_t)src >> 32), l) << 32);
+            const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + 2 * lane;
+            const int nr = popc32(mp);
+            uint32_t t = mp;
+            uint32_t r[kPage];
+#pragma unroll
+            for (int k = 0; k < kPage; ++k) {
+                const int p = t != 0u ? __builtin_ctz(t) : 0;
+                t &= t - 1u;
+                r[k] = k < nr ? *reinterpret_cast<const uint32_t*>(s + p * a.s_p) : 0u;
+            }
+#pragma unroll
+            for (int k = 0; k < kPage; ++k)
+                if (k < nr && (int64_t)op + k < a.cap)
+                    *reinterpret_cast<uint32_t*>(a.raw + ((int64_t)op + k) * 128 + 2 * lane) = r[k];
+        }
     }
 }
 
+template <bool PAGED, bool VEC16>
+__global__ void __launch_bounds__(1024) scan_write_kernel(EncArgs a, int nunits) {
+    __shared__ int s_base;
+    if (threadIdx.x == 0) s_base = a.rowoff[first_page_of(a, blockIdx.x)];
+    const int u = blockIdx.x * kScanUnits + threadIdx.x;
+    int bi = 0, pg = 0, hk = 0;
+    int64_t page = 0;
+    uint32_t m = 0;
+    if (u < nunits) {
+        page = unit_page32<PAGED>(a, u, bi, pg, hk);
+        m = (uint32_t)a.rowmask[page];
+    }
+    int total;
+    const int off = block_excl_scan(popc32(m), total) + s_base;   // synchronises: s_base is read
+    if (u < nunits) a.rowoff[page] = off;
+    copy_escaped_rows<VEC16>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, threadIdx.x & 63);
+}
+
 static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
-    const int64_t nb = (n + kScanUnits - 1) / kScanUnits;
-    hipLaunchKernelGGL(scan_count_kernel, dim3((unsigned)nb), dim3(1024), 0, stream, a, n);
-    hipLaunchKernelGGL(scan_blocks_kernel, dim3(1), dim3(1024), 0, stream, a, nb);
-    hipLaunchKernelGGL(scan_write_kernel, dim3((unsigned)nb), dim3(1024), 0, stream, a, n);
+    const unsigned nb = (unsigned)((n + kScanUnits - 1) / kScanUnits);
+    const bool paged = a.dst_pages != nullptr;
+    const bool vec16 = (uintptr_t)a.src % 16 == 0 && a.s_b % 8 == 0 && a.s_pg % 8 == 0 && a.s_p % 8 == 0 &&
+                       a.s_h % 8 == 0;
+    if (paged)
+        hipLaunchKernelGGL(scan_count_kernel<true>, dim3(nb), dim3(1024), 0, stream, a, (int)n);
+    else
+        hipLaunchKernelGGL(scan_count_kernel<false>, dim3(nb), dim3(1024), 0, stream, a, (int)n);
+    hipLaunchKernelGGL(scan_blocks_kernel, dim3(1), dim3(1024), 0, stream, a, (int64_t)nb);
+    auto k = paged ? (vec16 ? scan_write_kernel<true, true> : scan_write_kernel<true, false>)
+                   : (vec16 ? scan_write_kernel<false, true> : scan_write_kernel<false, false>);
+    hipLaunchKernelGGL(k, dim3(nb), dim3(1024), 0, stream, a, (int)n);
 }
 
 // Copy one page's raw rows (token p's row at src + p*s_p) into slots rowoff + k (< cap).
@@ -293,18 +332,6 @@ __device__ inline void copy_raw_rows(const uint16_t* src, int64_t s_p, uint32_t 
         d[lane] = s[lane];
         d[lane + 64] = s[lane + 64];
     }
-}
-
-__global__ void __launch_bounds__(256) rawcopy_kernel(EncArgs a, int64_t nunits) {
-    const int lane = threadIdx.x & 63;
-    const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (u >= nunits) return;
-    int bi, pg, hk;
-    unit_coords(a, u, bi, pg, hk);
-    const int64_t page = unit_page(a, bi, pg, hk);
-    const uint32_t m = (uint32_t)a.rowmask[page];
-    if (m == 0) return;
-    copy_raw_rows(a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, a.s_p, m, a.rowoff[page], a.cap, a.raw, lane);
 }
 
 // ---------------------------------------------------------------- device-side append
@@ -636,12 +663,13 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
                  "encode_pages: source rows must start at even elements (4-byte aligned)");
     const int64_t n = (int64_t)nb * npg * H;
     if (n == 0) return EXKV_OK;
+    EXKV_REQUIRE(n <= INT32_MAX - 1024, "encode_pages: %lld pages x heads in one call (limit 2^31 - 1025)",
+                 (long long)n);
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
     const unsigned grid = (unsigned)((n + 3) / 4);
     hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     launch_scan(a, n, stream);
-    hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     return launch_status("encode_pages");
 }
 
@@ -666,6 +694,8 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
                  "encode_pages_paged: source rows must start at even elements (4-byte aligned)");
     const int64_t n = (int64_t)nb * npg * H;
     if (n == 0) return EXKV_OK;
+    EXKV_REQUIRE(n <= INT32_MAX - 1024, "encode_pages_paged: %lld pages x heads in one call (limit 2^31 - 1025)",
+                 (long long)n);
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, 0, 0, nb, npg, H, TS};
     a.dst_pages = dst_pages;
@@ -674,7 +704,6 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     const unsigned grid = (unsigned)((n + 3) / 4);
     hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     launch_scan(a, n, stream);
-    hipLaunchKernelGGL(rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a, n);
     return launch_status("encode_pages_paged");
 }
 

@@ -122,3 +122,47 @@ def test_decode_partial_lengths(T):
     c = _gpu_encode(x)
     _say("decode T", T)
     assert same_bits(kernels.decode_to_bf16(c.buffers(), T), x[:, :T])
+
+
+@pytest.mark.parametrize("width,offset", [(128, 0), (130, 0), (136, 2)])
+def test_encoder_row_alignment(width, offset):
+    """Source rows inside wider rows: 16-byte aligned rows (width 128) take the wide raw-row
+    copy, 4-byte aligned ones (row pitch 130, or a 2-element offset) the narrow one; the
+    bytes equal the oracle's either way."""
+    x = synthetic.stress_pages(2, 64, 4, seed=21)
+    big = torch.zeros(2, 64, 4, width + offset, dtype=torch.bfloat16)
+    big[..., offset:offset + 128] = x
+    src = big.to(DEV)[..., offset:offset + 128]
+    _say("aligned encode", width, offset, src.stride())
+    ref = ocodec.encode(u16(x))
+    c = exactkv.CompressedKV(2, 64, 4, 128, reserve=1.0)
+    st = (src.stride(0), 16 * src.stride(1), src.stride(1), src.stride(2))
+    kernels.encode_pages(src, st, c._buf(), 0, 0, 2, 4)
+    assert ref["raw"].shape[0] > 0
+    _compare(c, ref, f"width {width} offset {offset}")
+
+
+def _popc16(t):
+    t = t.to(torch.int32)
+    return sum((t >> i) & 1 for i in range(16))
+
+
+@pytest.mark.parametrize("B,T,H", [(8, 8192, 16), (5, 8192, 32)])
+def test_encoder_slot_scan_full_size(B, T, H):
+    """65,536 units (the one-workgroup scan at its limit) and 81,920 units (the three-launch
+    scan), 5% outlier rows, counter starting at 7: every rowoff is 7 + the raw rows of the
+    units before it in (sequence, page, head) order, the counter ends at 7 + all of them,
+    and decoding gives back every bit."""
+    x = synthetic.make_kv(B, T, H, kind="k", seed=31, raw_row_rate=0.05, device=DEV)
+    _say("slot scan", B, T, H, "units", B * (T // 16) * H)
+    c = exactkv.CompressedKV(B, T, H, 128, reserve=0.08)
+    c.cnt.fill_(7)
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16)
+    per = _popc16(c.rowmask).flatten().to(torch.int64)
+    n = int(per.sum().item())
+    assert n > 0.04 * B * T * H
+    assert int(c.cnt.item()) == 7 + n and int(c._before.item()) == 7 and 7 + n <= c.cap
+    want = 7 + torch.cumsum(per, 0) - per
+    assert torch.equal(c.rowoff.flatten().to(torch.int64), want)
+    assert same_bits(kernels.decode_to_bf16(c.buffers(), T), x)

@@ -21,80 +21,96 @@ namespace exkv {
 
 __device__ inline uint8_t sm_byte(uint32_t u) { return (uint8_t)(((u >> 8) & 0x80u) | (u & 0x7Fu)); }
 
+// Two 16-bit lanes in one register: the page encoder keeps two channels' exponents per
+// register and works on both with packed integer ops (max, min, saturating subtract).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ inline u16x2 as_u16x2(uint32_t x) { return __builtin_bit_cast(u16x2, x); }
+__device__ inline uint32_t as_u32(u16x2 x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ inline u16x2 vmax(u16x2 a, u16x2 b) { return __builtin_elementwise_max(a, b); }
+__device__ inline u16x2 vmin(u16x2 a, u16x2 b) { return __builtin_elementwise_min(a, b); }
+__device__ inline u16x2 vsubs(u16x2 a, u16x2 b) { return __builtin_elementwise_sub_sat(a, b); }   // max(a - b, 0)
+// bytes 0 and 2 of x as a 16-bit value
+__device__ inline uint16_t bytes02(uint32_t x) { return (uint16_t)__builtin_amdgcn_perm(0u, x, 0x0c0c0200u); }
+
 // Encode one 16-token page of one head. Lane l = (half, m): tokens 8*half .. 8*half+7,
-// channels 2m, 2m+1, 2m+64 and 2m+65 -- so each code byte (channel j low nibble, j + 64
-// high nibble) and each pair of sm / code bytes is produced by one lane, and every load and
-// store moves two channels (half the instructions of one channel per lane). The two halves
-// combine their per-channel maxima with one cross-half shuffle. Token p's source row is
-// src + p * s_p, except row 15 which comes from `last` when given; rows must be 4-byte
-// aligned (even element offsets: callers check). Destination rows of consecutive tokens
-// are `rs` rows apart (rs = H).
+// channels 2m, 2m+1 (word lo) and 2m+64, 2m+65 (word hi) -- so each code byte (channel j
+// low nibble, j + 64 high nibble) and each pair of sm / code bytes is produced by one lane,
+// and every load and store moves two channels. Per channel, with e the 8-bit exponent:
+//   top = max e over the 16 tokens, floor = max(top - 15, 0), zf = (some e == 0) && floor > 0,
+//   nibble = max(e - floor, 0) (e <= top keeps it <= 15; e == 0 gives 0 either way),
+//   a row is raw if some channel has e != 0 && e < floor + zf, or if any floor >= 128;
+// the same rule as the reference's per-element test (code >= 1 for a non-zero in a
+// flagged group, code >= 0 otherwise, floor < 128), in packed 16-bit integer arithmetic.
+// The two halves combine their per-channel maxima and minima with one cross-half shuffle
+// each. Token p's source row is src + p * s_p, except row 15 which comes from `last` when
+// given; rows must be 4-byte aligned (even element offsets: callers check). Destination
+// rows of consecutive tokens are `rs` rows apart (rs = H).
 __device__ __attribute__((always_inline)) inline void encode_page(const uint16_t* src, int64_t s_p,
                                                                   const uint16_t* last, int lane,
-                            uint8_t* sm0, uint8_t* code0, int64_t rs, uint8_t* basep, int32_t* rmaskp) {
+                                                                  uint8_t* sm0, uint8_t* code0, int64_t rs,
+                                                                  uint8_t* basep, int32_t* rmaskp) {
     const int half = lane >> 5, m = lane & 31;
+    // per-lane row-0 addresses of the lane's half; token i of the half is i strides on
+    const uint16_t* srow = src + (int64_t)(8 * half) * s_p + 2 * m;
+    const int64_t sm_stride = rs * 128, code_stride = rs * 64;
+    uint8_t* smrow = sm0 + (int64_t)(8 * half) * sm_stride + 2 * m;
+    uint8_t* coderow = code0 + (int64_t)(8 * half) * code_stride + 2 * m;
     uint32_t lo[8], hi[8];                             // bf16 pairs: channels (2m, 2m+1), (2m+64, 2m+65)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int p = 8 * half + i;
-        const uint16_t* rp = (p == kPage - 1 && last != nullptr) ? last : src + p * s_p;
-        lo[i] = *reinterpret_cast<const uint32_t*>(rp + 2 * m);
-        hi[i] = *reinterpret_cast<const uint32_t*>(rp + 64 + 2 * m);
+        const uint16_t* rp = (i == 7 && half == 1 && last != nullptr) ? last + 2 * m : srow + i * s_p;
+        lo[i] = *reinterpret_cast<const uint32_t*>(rp);
+        hi[i] = *reinterpret_cast<const uint32_t*>(rp + 64);
     }
-    // per channel c (0: 2m, 1: 2m+1, 2: 2m+64, 3: 2m+65): exponent window over 16 tokens
-    auto ex = [&](int i, int c) -> int {
-        const uint32_t w = c < 2 ? lo[i] : hi[i];
-        return (int)((w >> (c & 1 ? 23 : 7)) & 255u);
-    };
-    int top[4] = {0, 0, 0, 0}, zer[4] = {0, 0, 0, 0};
+    u16x2 elo[8], ehi[8];                              // exponents, one channel per 16-bit lane
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int e = ex(i, c);
-            top[c] = max(top[c], e);
-            zer[c] |= e == 0;
-        }
-    int fl[4];
-    bool zf[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        top[c] = max(top[c], __shfl_xor(top[c], 32));
-        zer[c] |= __shfl_xor(zer[c], 32);
-        fl[c] = max(top[c] - 15, 0);
-        zf[c] = zer[c] && fl[c] > 0;
+    for (int i = 0; i < 8; ++i) {
+        elo[i] = as_u16x2((lo[i] >> 7) & 0x00FF00FFu);
+        ehi[i] = as_u16x2((hi[i] >> 7) & 0x00FF00FFu);
     }
+    u16x2 tlo = elo[0], thi = ehi[0], nlo = elo[0], nhi = ehi[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+        tlo = vmax(tlo, elo[i]);
+        thi = vmax(thi, ehi[i]);
+        nlo = vmin(nlo, elo[i]);
+        nhi = vmin(nhi, ehi[i]);
+    }
+    tlo = vmax(tlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(tlo), 32)));
+    thi = vmax(thi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(thi), 32)));
+    nlo = vmin(nlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nlo), 32)));
+    nhi = vmin(nhi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nhi), 32)));
+    const u16x2 c15 = {15, 15}, one = {1, 1};
+    const u16x2 flo = vsubs(tlo, c15), fhi = vsubs(thi, c15);                 // floors
+    const u16x2 zlo = vmin(vsubs(one, nlo), vmin(flo, one));                  // zero flags (0 / 1)
+    const u16x2 zhi = vmin(vsubs(one, nhi), vmin(fhi, one));
+    const u16x2 glo = flo + zlo, ghi = fhi + zhi;                             // non-zero e below: raw
     uint32_t esc = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int p = 8 * half + i;
-        int nib[4];
-        bool ok = true;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int e = ex(i, c);
-            const int cd = (zf[c] && e == 0) ? 0 : e - fl[c];
-            ok = ok && fl[c] < 128 && cd >= ((zf[c] && e != 0) ? 1 : 0);
-            nib[c] = min(max(cd, 0), 15);
-        }
-        esc |= (uint32_t)!ok << i;
-        // sm bytes of the two pairs, and the code bytes 2m (nib 0 | nib 2 << 4), 2m+1 (1 | 3)
-        const uint32_t smlo = ((lo[i] >> 8) & 0x80u) | (lo[i] & 0x7Fu) | (((lo[i] >> 24) & 0x80u) | ((lo[i] >> 16) & 0x7Fu)) << 8;
-        const uint32_t smhi = ((hi[i] >> 8) & 0x80u) | (hi[i] & 0x7Fu) | (((hi[i] >> 24) & 0x80u) | ((hi[i] >> 16) & 0x7Fu)) << 8;
-        uint8_t* sp = sm0 + p * rs * 128;
-        *reinterpret_cast<uint16_t*>(sp + 2 * m) = (uint16_t)smlo;
-        *reinterpret_cast<uint16_t*>(sp + 64 + 2 * m) = (uint16_t)smhi;
-        *reinterpret_cast<uint16_t*>(code0 + p * rs * 64 + 2 * m) =
-            (uint16_t)((nib[0] | (nib[2] << 4)) | ((nib[1] | (nib[3] << 4)) << 8));
+        const uint32_t dlo = as_u32(vmin(vsubs(glo, elo[i]), elo[i]));
+        const uint32_t dhi = as_u32(vmin(vsubs(ghi, ehi[i]), ehi[i]));
+        esc |= (uint32_t)((dlo | dhi) != 0u) << i;
+        // code bytes 2m (nibble of 2m | nibble of 2m+64 << 4) and 2m+1 (2m+1 | 2m+65 << 4)
+        const uint32_t cw = as_u32(vsubs(elo[i], flo)) | (as_u32(vsubs(ehi[i], fhi)) << 4);
+        // sm bytes: sign over bit 7 of each bf16's mantissa byte
+        const uint32_t slo = (lo[i] & 0x007F007Fu) | ((lo[i] >> 8) & 0x00800080u);
+        const uint32_t shi = (hi[i] & 0x007F007Fu) | ((hi[i] >> 8) & 0x00800080u);
+        uint8_t* sp = smrow + i * sm_stride;
+        *reinterpret_cast<uint16_t*>(sp) = bytes02(slo);
+        *reinterpret_cast<uint16_t*>(sp + 64) = bytes02(shi);
+        *reinterpret_cast<uint16_t*>(coderow + i * code_stride) = bytes02(cw);
     }
     if (half == 0) {
-        const uint32_t b0 = (uint32_t)min(fl[0] + (zf[0] ? 128 : 0), 255), b1 = (uint32_t)min(fl[1] + (zf[1] ? 128 : 0), 255);
-        const uint32_t b2 = (uint32_t)min(fl[2] + (zf[2] ? 128 : 0), 255), b3 = (uint32_t)min(fl[3] + (zf[3] ? 128 : 0), 255);
-        *reinterpret_cast<uint16_t*>(basep + 2 * m) = (uint16_t)(b0 | (b1 << 8));
-        *reinterpret_cast<uint16_t*>(basep + 64 + 2 * m) = (uint16_t)(b2 | (b3 << 8));
+        const u16x2 c128 = {128, 128}, c255 = {255, 255};
+        const uint32_t blo = as_u32(vmin(flo + zlo * c128, c255)), bhi = as_u32(vmin(fhi + zhi * c128, c255));
+        *reinterpret_cast<uint16_t*>(basep + 2 * m) = bytes02(blo);
+        *reinterpret_cast<uint16_t*>(basep + 64 + 2 * m) = bytes02(bhi);
     }
-    // rowmask: ballot bit l < 32 is token i (half 0), bit 32 + l token 8 + i
-    uint32_t rm = 0;
+    // rowmask: ballot bit l < 32 is token i (half 0), bit 32 + l token 8 + i; a floor of
+    // 128 or more in any channel makes every row raw
+    const bool big = ((as_u32(flo) | as_u32(fhi)) & 0xFF80FF80u) != 0u;
+    uint32_t rm = __ballot(big) != 0 ? 0xFFFFu : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint64_t bal = __ballot((esc >> i) & 1u);
@@ -142,15 +158,17 @@ __device__ inline int64_t unit_page(const EncArgs& a, int bi, int pg, int hk) {
     return unit_pidx(a, bi, pg) * a.H + hk;
 }
 
-__global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int64_t nunits) {
+// One wavefront per unit (sequence, page, head); the unit's coordinates and addresses are
+// wavefront-uniform (scalar arithmetic, 32-bit: unit counts are below 2^31).
+__global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int nunits) {
     const int lane = threadIdx.x & 63;
-    const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int u = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (u >= nunits) return;
-    int bi, pg, hk;
-    unit_coords(a, u, bi, pg, hk);
-    const uint16_t* src = a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h;
-    const int64_t row0 = unit_pidx(a, bi, pg) * kPage * a.H + hk;
-    const int64_t page = unit_page(a, bi, pg, hk);
+    const uint32_t q = (uint32_t)u / (uint32_t)a.H, bi = q / (uint32_t)a.npg;
+    const int hk = u - (int)(q * (uint32_t)a.H), pg = (int)(q - bi * (uint32_t)a.npg);
+    const uint16_t* src = a.src + (int64_t)bi * a.s_b + (int64_t)pg * a.s_pg + (int64_t)hk * a.s_h;
+    const int64_t pidx = unit_pidx(a, (int)bi, pg);
+    const int64_t row0 = pidx * kPage * a.H + hk, page = pidx * a.H + hk;
     encode_page(src, a.s_p, nullptr, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
                 a.rowmask + page);
 }
@@ -668,7 +686,7 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
     const unsigned grid = (unsigned)((n + 3) / 4);
-    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, (int)n);
     launch_scan(a, n, stream);
     return launch_status("encode_pages");
 }
@@ -702,7 +720,7 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     a.dst_stride = dst_stride;
     a.all_pages = (int64_t)B * (TS / kPage);
     const unsigned grid = (unsigned)((n + 3) / 4);
-    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, n);
+    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, (int)n);
     launch_scan(a, n, stream);
     return launch_status("encode_pages_paged");
 }

@@ -250,7 +250,8 @@ def main():
                     help="sliding-window attention over each sequence's last WINDOW tokens (0: all)")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
-                         "then a few launches of each attention kernel; no timing")
+                         "then a few launches of each attention kernel (with --workload c3: of the encoder "
+                         "over the prefill's keys); no timing")
     a = ap.parse_args()
     if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"):
         if a.gpus != 1:
@@ -515,15 +516,23 @@ def wire_bench(a):
     print(json.dumps(res), flush=True)
 
 
+def calibration_copy(dev):
+    """The copy kernel that counter runs scale FETCH_SIZE / WRITE_SIZE by: torch.mul over
+    64 Mi fp32 (256 MiB read + 256 MiB written). Returns the bytes read (= written)."""
+    import torch
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    return n * 4
+
+
 def profile_run(kernels, q, kc, vc, kb, vb, T, ns, sl, out):
     """Launch sequence for hardware-counter runs: the calibration copy, then 5 launches each
     of the compressed split kernel, the bf16 split kernel and the full compressed call."""
     import torch
-    n = 64 << 20                                             # 64 Mi floats: 256 MiB read + 256 MiB written
-    src = torch.ones(n, dtype=torch.float32, device=q.device)
-    dst = torch.empty_like(src)
-    torch.mul(src, 1.0, out=dst)
-    torch.cuda.synchronize()
+    nbytes = calibration_copy(q.device)
     for _ in range(5):
         split_only(kernels, q, kc, vc, T, ns, sl, True)
     for _ in range(5):
@@ -531,8 +540,28 @@ def profile_run(kernels, q, kc, vc, kb, vb, T, ns, sl, out):
     for _ in range(5):
         kernels.attention_compressed(q, kc, vc, T, nsplit=ns, split_len=sl, out=out)
     torch.cuda.synchronize()
-    print(json.dumps({"profile_run": True, "copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
+    print(json.dumps({"profile_run": True, "copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
                       "nsplit": ns, "split_len": sl}), flush=True)
+
+
+def encoder_profile_run(exactkv, kernels, x):
+    """Launch sequence for hardware-counter runs of the encoder: the calibration copy, then
+    5 encodes of every page of x (one exkv_encode_pages call each, counter reset between)."""
+    import torch
+    nbytes = calibration_copy(x.device)
+    B, TS, H, D = x.shape
+    st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+    c = exactkv.CompressedKV(B, TS, H, D, reserve=0.05)
+    for _ in range(5):
+        c.cnt.zero_()
+        kernels.encode_pages(x, st, c._buf(), 0, 0, B, TS // 16)
+    torch.cuda.synchronize()
+    rows = B * TS * H
+    print(json.dumps({"profile_run": True, "copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "encode_units": B * (TS // 16) * H, "source_bytes": rows * 256,
+                      "raw_rows": int(c.cnt.item()),
+                      "algorithmic_bytes": rows * 256 + rows * 192 + rows // 16 * 136 + int(c.cnt.item()) * 256}),
+          flush=True)
 
 
 def c3_stress(a):
@@ -552,6 +581,9 @@ def c3_stress(a):
     k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=100, device=dev, raw_row_rate=6e-3)
     v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=101, device=dev, raw_row_rate=6e-3)
     q = synthetic.make_q(B, Hq, seed=102, device=dev)
+    if a.profile:                                      # counter run of the encoder over the keys
+        encoder_profile_run(exactkv, kernels, k)
+        return
     enc = encoder_gbps(exactkv, kernels, [k, v], TS, a.steps, a.warmup)
     print("[c3] encoder timed", file=sys.stderr, flush=True)
     kcs, vcs, kbs, vbs, grows = [], [], [], [], []

@@ -292,10 +292,13 @@ def _check_source(src, strides, nb, npg, H):
 
 
 def encode_pages(src, strides, buf, b0, pg0, nb, npg):
-    """Encode nb sequences x npg pages. src points at sequence b0's first page to encode;
-    strides = (seq, page, token, head) in elements. buf: dict with sm, code, base, rowmask,
-    rowoff, raw, cnt, cap, TS, H, D (optionally 'before', the counter before the call).
-    Raw rows get slots in (sequence, page, head, token) order from the counter on."""
+    """Page encoder (reference kernels.py:216-268, same arguments). Source page pg0 + p of
+    sequence b0 + i sits at src + i*s_b + p*s_pg, its token rows s_p apart and heads s_h
+    apart, with (s_b, s_pg, s_p, s_h) = strides in elements; it is written to page pg0 + p
+    of cache sequence b0 + i. buf is a cache's encoder view (CompressedKV._buf()): the six
+    arrays, the raw-row counter cnt, cap, TS, H, D and optionally 'before', which receives
+    the counter's value before the call. Escaped rows take pool slots from the counter on,
+    in (sequence, page, head, token) order."""
     H, TS, D = buf["H"], buf["TS"], buf["D"]
     _check_source(src, strides, nb, npg, H)
     raw = buf["raw"]

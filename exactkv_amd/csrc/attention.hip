@@ -127,9 +127,9 @@ struct AttnArgs {
 };
 
 // ---- split merge (kernels.py:33-43): M = max_s m_s, w_s = 2^(m_s - M),
-// out = sum_s o_s w_s / sum_s l_s w_s, one wavefront per (sequence, query head) row with
-// lane = channel pair. Shared by the fused merge and attn_reduce_kernel so both produce
-// the same bits: the sums run over s in order with explicit fmas.
+// out = sum_s o_s w_s / sum_s l_s w_s. Up to 32 splits: one wavefront per (sequence, query
+// head) row with lane = channel pair, the sums over s in order with explicit fmas -- the
+// order of the fused merge's one-level case, so both produce the same bits.
 __device__ inline float fast_exp2(float x);
 __device__ inline float wave_max(float x) {
 #pragma unroll
@@ -139,24 +139,6 @@ __device__ inline float wave_max(float x) {
 __device__ inline uint32_t pack_bf16x2(float a, float b) {
     const __bf16 r0 = (__bf16)a, r1 = (__bf16)b;
     return (uint32_t)__builtin_bit_cast(uint16_t, r0) | ((uint32_t)__builtin_bit_cast(uint16_t, r1) << 16);
-}
-// Accumulate splits [c, c + n) (n <= 32): o loads all in flight together; w and l of split
-// c + i sit in lane i of ws / ls.
-__device__ __attribute__((always_inline)) inline void merge_chunk(const float2* po2, int c, int n, float ws, float ls, int lane, float& n0,
-                                   float& n1, float& den) {
-    float2 o[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i)
-        if (i < n) o[i] = po2[(int64_t)(c + i) * (kD / 2) + lane];
-#pragma unroll
-    for (int i = 0; i < 32; ++i)
-        if (i < n) {
-            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), i));
-            const float lv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), i));
-            n0 = __builtin_fmaf(o[i].x, w, n0);
-            n1 = __builtin_fmaf(o[i].y, w, n1);
-            den = __builtin_fmaf(lv, w, den);
-        }
 }
 // ns <= N splits in one round trip: m, l and o loads issued together.
 template <int N>
@@ -183,23 +165,6 @@ __device__ __attribute__((always_inline)) inline uint32_t merge_direct(const flo
         }
     return pack_bf16x2(n0 / den, n1 / den);
 }
-__device__ __attribute__((always_inline)) inline uint32_t merge_row(const float* po, const float* m, const float* l,
-                                                                     int ns, int lane) {
-    if (ns <= 32) return merge_direct<32>(po, m, l, ns, lane);
-    const float2* po2 = reinterpret_cast<const float2*>(po);
-    float mm = -INFINITY;
-    for (int s = lane; s < ns; s += 64) mm = fmaxf(mm, m[s]);
-    const float M = wave_max(mm);
-    float n0 = 0.f, n1 = 0.f, den = 0.f;
-    for (int c = 0; c < ns; c += 32) {
-        const int n = ns - c < 32 ? ns - c : 32;
-        const float ws = lane < n ? fast_exp2(m[c + lane] - M) : 0.f;
-        const float ls = lane < n ? l[c + lane] : 0.f;
-        merge_chunk(po2, c, n, ws, ls, lane, n0, n1, den);
-    }
-    return pack_bf16x2(n0 / den, n1 / den);
-}
-
 __device__ inline bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     u32x4 u = {a, b, c, d};
     return __builtin_bit_cast(bf16x8, u);
@@ -983,46 +948,85 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     merge_tail(a, b, hb, hg, gh, split);
 }
 
-// Separate merge of the split partials, one workgroup per (sequence, query head) row.
-// Up to 32 splits: one wavefront, every load of the row in flight at once (the fused
-// merge's code, so both give the same bits). More: kReduceWaves wavefronts each take a
-// contiguous range of splits (one round trip per 32 of them) under the common M, and
-// wavefront 0 adds their sums in wavefront order.
-constexpr int kReduceWaves = 8;
-__global__ void __launch_bounds__(64 * kReduceWaves) attn_reduce_kernel(const float* po, const float* pm,
-                                                                        const float* pl, uint16_t* out, int ns) {
+// Separate merge of up to 32 splits: one wavefront per (sequence, query head) row, every
+// load of the row in flight at once (the fused merge's code, so both give the same bits).
+__global__ void __launch_bounds__(64) attn_reduce_kernel(const float* po, const float* pm, const float* pl,
+                                                         uint16_t* out, int ns) {
     const int64_t row = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const float* o = po + row * ns * kD;
+    const int lane = threadIdx.x & 63;
+    reinterpret_cast<uint32_t*>(out + row * kD)[lane] =
+        merge_direct<32>(po + row * ns * kD, pm + row * ns, pl + row * ns, ns, lane);
+}
+
+// Separate merge of more than 32 splits: workgroup (row, 16-channel chunk) of four
+// wavefronts, so that a row's loads spread over eight workgroups (rows x 8 of them fill
+// the chip where rows alone would use a few CUs). Lane (split group sg = lane / 8, channel
+// pair cp = lane % 8); wavefront w takes a contiguous quarter of the splits, eight at a
+// time, all loads of a batch in flight together; the sums combine over sg by shuffles,
+// then over the wavefronts in order through LDS. Deterministic, so the compressed call and
+// its twin still agree bit for bit.
+constexpr int kWideWaves = 4, kWideChunk = 16;
+__global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const float* po, const float* pm,
+                                                                            const float* pl, uint16_t* out, int ns) {
+    const int64_t row = blockIdx.x;
+    const int c0 = kWideChunk * (int)blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sg = lane >> 3, cp = lane & 7;
+    const float* o = po + row * ns * kD + c0 + 2 * cp;
     const float* m = pm + row * ns;
     const float* l = pl + row * ns;
-    if (nw == 1) {
-        reinterpret_cast<uint32_t*>(out + row * kD)[lane] = merge_row(o, m, l, ns, lane);
-        return;
-    }
+    __shared__ float smax[kWideWaves];
+    __shared__ float part[kWideWaves][3][8];
     float mm = -INFINITY;
-    for (int s = lane; s < ns; s += 64) mm = fmaxf(mm, m[s]);
-    const float M = wave_max(mm);
-    const int per = (ns + nw - 1) / nw, c0 = min(ns, wave * per), c1 = min(ns, c0 + per);
-    float n0 = 0.f, n1 = 0.f, den = 0.f;
-    for (int c = c0; c < c1; c += 32) {
-        const int n = c1 - c < 32 ? c1 - c : 32;
-        const float ws = lane < n ? fast_exp2(m[c + lane] - M) : 0.f;
-        const float ls = lane < n ? l[c + lane] : 0.f;
-        merge_chunk(reinterpret_cast<const float2*>(o), c, n, ws, ls, lane, n0, n1, den);
-    }
-    __shared__ float part[kReduceWaves][3][64];
-    part[wave][0][lane] = n0;
-    part[wave][1][lane] = n1;
-    part[wave][2][lane] = den;
+    for (int s = threadIdx.x; s < ns; s += 64 * kWideWaves) mm = fmaxf(mm, m[s]);
+    mm = wave_max(mm);
+    if (lane == 0) smax[wave] = mm;
     __syncthreads();
-    if (wave == 0) {
-        for (int w = 1; w < nw; ++w) {
-            n0 += part[w][0][lane];
-            n1 += part[w][1][lane];
-            den += part[w][2][lane];
+    float M = smax[0];
+#pragma unroll
+    for (int w = 1; w < kWideWaves; ++w) M = fmaxf(M, smax[w]);
+    const int per = (ns + kWideWaves - 1) / kWideWaves;
+    const int s0 = min(ns, wave * per), s1 = min(ns, s0 + per);
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+    for (int b0 = s0; b0 < s1; b0 += 64) {
+        float2 v[8];
+        float mv[8], lv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int s = min(b0 + 8 * i + sg, s1 - 1);           // past the range: a valid split, weight 0
+            v[i] = *reinterpret_cast<const float2*>(o + (int64_t)s * kD);
+            mv[i] = m[s];
+            lv[i] = l[s];
         }
-        reinterpret_cast<uint32_t*>(out + row * kD)[lane] = pack_bf16x2(n0 / den, n1 / den);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float w = b0 + 8 * i + sg < s1 ? fast_exp2(mv[i] - M) : 0.f;
+            n0 = __builtin_fmaf(v[i].x, w, n0);
+            n1 = __builtin_fmaf(v[i].y, w, n1);
+            den = __builtin_fmaf(lv[i], w, den);
+        }
+    }
+#pragma unroll
+    for (int d = 8; d < 64; d <<= 1) {
+        n0 += __shfl_xor(n0, d);
+        n1 += __shfl_xor(n1, d);
+        den += __shfl_xor(den, d);
+    }
+    if (sg == 0) {
+        part[wave][0][cp] = n0;
+        part[wave][1][cp] = n1;
+        part[wave][2][cp] = den;
+    }
+    __syncthreads();
+    if (wave == 0 && sg == 0) {
+        float a0 = part[0][0][cp], a1 = part[0][1][cp], dn = part[0][2][cp];
+#pragma unroll
+        for (int w = 1; w < kWideWaves; ++w) {
+            a0 += part[w][0][cp];
+            a1 += part[w][1][cp];
+            dn += part[w][2][cp];
+        }
+        reinterpret_cast<uint32_t*>(out + row * kD + c0)[cp] = pack_bf16x2(a0 / dn, a1 / dn);
     }
 }
 
@@ -1100,8 +1104,11 @@ extern "C" int exkv_time_next_split(hipEvent_t start, hipEvent_t stop) {
 
 static int launch_reduce(const float* o, const float* m, const float* l, void* out, int64_t rows, int ns,
                          hipStream_t stream) {
-    const unsigned threads = ns <= 32 ? 64u : 64u * (unsigned)min(kReduceWaves, (ns + 31) / 32);
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rows), dim3(threads), 0, stream, o, m, l, (uint16_t*)out, ns);
+    if (ns <= 32)
+        hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rows), dim3(64), 0, stream, o, m, l, (uint16_t*)out, ns);
+    else
+        hipLaunchKernelGGL(attn_reduce_wide_kernel, dim3((unsigned)rows, kD / kWideChunk), dim3(64 * kWideWaves), 0,
+                           stream, o, m, l, (uint16_t*)out, ns);
     return hip_status(hipGetLastError(), "attn_reduce");
 }
 

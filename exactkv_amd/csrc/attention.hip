@@ -914,31 +914,35 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         ml[wave * 16 + r] = l_t;
     }
     __syncthreads();
-    // thread t merges (head slot, head, channel) items; waves of one head slot s are s, s + HW, ...
-    for (int idx = threadIdx.x; idx < a.HW * gh * kD; idx += kThreads) {
-        const int d = idx & (kD - 1);
-        const int h = (idx >> 7) % gh;
-        const int hs = (idx >> 7) / gh;
+    // thread t merges (head slot, head, 4-channel group) items, four channels with the same
+    // per-channel arithmetic as one; waves of one head slot s are s, s + HW, ...
+    for (int idx = threadIdx.x; idx < a.HW * gh * (kD / 4); idx += kThreads) {
+        const int d = 4 * (idx & (kD / 4 - 1));
+        const int h = (idx >> 5) % gh;
+        const int hs = (idx >> 5) / gh;
         float M = -INFINITY;
         for (int ph = 0; ph < nphase; ++ph) M = fmaxf(M, mm[(ph * a.HW + hs) * 16 + h]);
-        float o = 0.f, l = 0.f;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        float l = 0.f;
         if (M != -INFINITY) {
             for (int ph = 0; ph < nphase; ++ph) {
                 const int w = ph * a.HW + hs;
                 const float wt = fast_exp2(mm[w * 16 + h] - M);
-                o += wt * mo[(w * 16 + h) * kD + d];
+                const f32x4 v = *reinterpret_cast<const f32x4*>(mo + (w * 16 + h) * kD + d);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o[c] += wt * v[c];
                 l += wt * ml[w * 16 + h];
             }
         }
         const int64_t prow = ((int64_t)b * a.Hq + (int64_t)(hb * a.HW + hs) * a.G + hg * 16 + h) * a.nsplit + split;
         if (a.counters == nullptr) {
-            a.part_o[prow * kD + d] = o;
+            *reinterpret_cast<f32x4*>(a.part_o + prow * kD + d) = o;
             if (d == 0) {
                 a.part_m[prow] = M;
                 a.part_l[prow] = l;
             }
         } else {
-            st_dev(a.part_o + prow * kD + d, o);
+            st_dev4(a.part_o + prow * kD + d, o);
             if (d == 0) {
                 st_dev(a.part_m + prow, M);
                 st_dev(a.part_l + prow, l);

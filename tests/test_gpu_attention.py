@@ -226,3 +226,27 @@ def test_sliding_window_paged_and_bad_arguments():
     with pytest.raises(RuntimeError, match="cover"):
         kernels.attention_reference(q1, kd[:, :512].contiguous(), vd[:, :512].contiguous(), 500, window=200,
                                     nsplit=1, split_len=192)
+
+
+@pytest.mark.parametrize("ns", [1, 7, 32, 33, 63, 200, 1000])
+def test_merge_kernel_against_oracle(ns):
+    """exkv_attn_reduce on synthetic partials (some splits empty: m = -inf, l = 0, o = 0):
+    the one-wavefront merge up to 32 splits and the (row, channel chunk) merge above, against
+    the oracle's LSE merge (reference kernels.py:33-43), within one bf16 rounding step."""
+    from exactkv_amd import _lib
+    rows, D = 5, 128
+    rng = np.random.default_rng(ns)
+    m = (rng.standard_normal((rows, ns)) * 4).astype(np.float32)
+    l = rng.uniform(1, 5, (rows, ns)).astype(np.float32)
+    o = (rng.standard_normal((rows, ns, D)) * l[..., None]).astype(np.float32)
+    empty = rng.random((rows, ns)) < 0.2
+    empty[:, 0] = False                                 # every row keeps one non-empty split
+    m[empty], l[empty], o[empty] = -np.inf, 0.0, 0.0
+    _say("merge", ns)
+    wo, wm, wl = (torch.from_numpy(x).to(DEV) for x in (o, m, l))
+    out = torch.empty(rows, D, dtype=torch.bfloat16, device=DEV)
+    _lib.call("exkv_attn_reduce", _lib.ptr(wo), _lib.ptr(wm), _lib.ptr(wl), _lib.ptr(out), rows, ns, D,
+              _lib.stream())
+    ref = oatt.merge_splits(m, l, o)
+    got = out.float().cpu().numpy()
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30), np.abs(got - ref).max()

@@ -670,13 +670,16 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         dma4(a.v.rowmask + page, mst + 512u);
         dma4(a.v.rowoff + page, mst + 768u);
     }
-    // the first pages' bytes go out before their metadata is known: their raw-row loads follow
-    // once the page table has landed, so no scalar round trip sits before the first loads
+    // The first page's bytes go out before its metadata is known; its raw-row load follows
+    // once the page table has landed. The compressed kernel issues the second page only
+    // then: every wavefront's first burst is issued at once at the start, and its DMAs stall
+    // at issue while the CU's memory pipeline is full, so a shorter first burst gets each
+    // wavefront's first page in sooner (issue done at a median 1.9 instead of 3.7 us at c2a).
     if (npw > 0) issue_bytes(0, ring);
-    if (NST == 3 && npw > 1) issue_bytes(1, ring + STB);
+    if (!COMP && NST == 3 && npw > 1) issue_bytes(1, ring + STB);
     // q and the page table have landed once only the first pages' byte loads are in flight
     constexpr int kBytesPerPage = COMP ? kDmaPerPage[1] - 1 : kDmaPerPage[0];
-    const int first = min(npw, NST - 1);
+    const int first = COMP ? min(npw, 1) : min(npw, NST - 1);
     if (first >= 2)
         wait_vm<2 * kBytesPerPage>();
     else if (first == 1)
@@ -706,19 +709,19 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers before their stage is reused
     if constexpr (COMP) {
         if (npw > 0) issue_raw(0, meta(0));
+        if (npw > 1) issue_bytes(1, ring + STB);
         if (npw > 1) issue_raw(1, meta(1));
     }
 
     progress[wave] = 0;
     int stg = 0;                                       // stage of page j (j % NST)
     for (int j = 0; j < npw; ++j) {
-        // stage j is complete once only page j + 1's loads are in flight. The prologue issued
-        // page 0's bytes, page 1's bytes, then their raw-row loads: page 0 is in once only
-        // page 1's raw-row load is (or, without a raw-row load of its own, page 1's bytes too).
+        // stage j is complete once only page j + 1's loads are in flight (its bytes, then its
+        // raw-row load, issued after page j's raw-row load -- in the prologue too)
         if (NST == 3 && j + 1 < npw) {
             if constexpr (COMP) {
                 const int next = raw_loads(meta(j + 1));
-                wait_vm_n(j > 0 ? kDmaPerPage[1] - 1 + next : (raw_loads(meta(0)) ? next : kDmaPerPage[1] - 1 + next));
+                wait_vm_n(kDmaPerPage[1] - 1 + next);
             } else {
                 wait_vm<kDmaPerPage[COMP]>();
             }

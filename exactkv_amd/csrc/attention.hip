@@ -3,10 +3,11 @@
 // Reference: exactkv/kernels.py _split_c_kernel :142-165, _split_ref_kernel :168-194,
 // _attn_block :46-59, _reduce_kernel :33-43.
 //
-// Grid: x = token split, y = (sequence, KV head, group of 16 query heads). A workgroup is
-// 8 wavefronts (one workgroup per CU: it owns ~150 KB of LDS). The wavefronts take the
-// split's 16-token pages round robin, each with its own online-softmax state, and are
-// merged through LDS at the end (one partial per split).
+// Grid: x = token split, y = (sequence, block of gcd(Hkv, 8) KV heads, group of 16 query
+// heads). A workgroup is 8 wavefronts (one workgroup per CU: it owns ~158 KB of LDS): each
+// KV head of the block gets 8 / gcd(Hkv, 8) of them ("page phases"), which take the split's
+// 16-token pages round robin, each with its own online-softmax state, and are merged
+// through LDS at the end (one partial per split and query head).
 //
 // Memory pipeline (per wavefront): each page is brought into a private LDS ring with a
 // fixed number (kDmaPerPage) of direct-to-LDS loads (global_load_lds_dwordx4/_dword), two
@@ -17,8 +18,8 @@
 //
 // Per page:
 //   * K and V are rebuilt bit-exactly in VGPRs from the staged bytes (tile.hpp), lane =
-//     token; raw rows are spliced in from loads issued before the next page's DMA (so the
-//     compiler's own wait for them counts only that younger batch).
+//     token; raw rows are spliced in from the wavefront's raw-row slots, which one more
+//     direct-to-LDS load per page fills (issued once the page's metadata is known).
 //   * S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (tokens = rows, the G query heads of the
 //     KV head = columns, padded to 16); online softmax in base 2, scores scaled by
 //     D^-1/2 log2(e), p rounded to bf16 for P.V, l summed from fp32 p.
@@ -47,10 +48,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kFusedMaxSplits = 1024;   // up to this many splits the split kernel can merge in its tail
-constexpr int kDmaPerPage[2] = {8, 8}; // direct-to-LDS loads per page: bf16, compressed (raw row included)
+constexpr int kDmaPerPage[2] = {8, 8}; // direct-to-LDS loads per page: bf16; compressed 7 + a raw-row load (pages with raw rows)
 
 // compressed page stage (bytes): K sm 16x128 | K code 16x64 | V sm | V code | K base,
-// V base (128 each); rowmask/rowoff come through the scalar cache instead
+// V base (128 each); rowmask/rowoff of the wavefront's pages are loaded once, up front
 constexpr int CS_KSM = 0, CS_KCODE = 2048, CS_VSM = 3072, CS_VCODE = 5120, CS_BASE = 6144, CS_BYTES = 6400;
 // bf16 page stage: K rows 16x256 | V rows 16x256
 constexpr int BS_K = 0, BS_V = 4096, BS_BYTES = 8192;

@@ -1,19 +1,22 @@
 // Page encoder, deterministic raw-slot assignment, device-side append and the
 // compressed -> bf16 decoder, for gfx950.
 //
-// Encoding one call's pages takes three launches on the caller's stream:
-//   1. enc_pages_kernel  one wavefront per (sequence, page, head): exponent window,
-//                        zero flag, codes, sign|mantissa bytes, base bytes, rowmask
-//                        (reference kernels.py:216-264, codec.py:31-49);
-//   2. the slot scan     rowoff = counter + exclusive running count of raw rows over the
-//                        call's pages in (sequence, page, head) order, in three launches
-//                        (block counts, a scan of the block totals, the writes); the
-//                        counter advances by the total (codec.py:50-53 order; the
-//                        reference GPU encoder used an atomic counter, kernels.py:262);
-//   3. rawcopy_kernel    copies raw rows into their slots, skipping slots >= cap
-//                        (kernels.py:265-268), so an overflow is seen from the counter.
-// The append path (cache.py:100-112) runs the same three steps with the token count
-// read from device memory, so a decode step can be captured in a HIP graph.
+// Encoding one call's pages takes four launches on the caller's stream:
+//   1. enc_pages_kernel    one wavefront per (sequence, page, head): exponent window,
+//                          zero flag, codes, sign|mantissa bytes, base bytes, rowmask
+//                          (reference kernels.py:216-264, codec.py:31-49);
+//   2. scan_count_kernel   per block of 1024 units, its raw rows;
+//   3. scan_blocks_kernel  the block totals scanned from the counter, which advances
+//                          by the total;
+//   4. scan_write_kernel   rowoff = counter + exclusive running count of raw rows over
+//                          the call's pages in (sequence, page, head) order (codec.py:50-53
+//                          order; the reference GPU encoder used an atomic counter,
+//                          kernels.py:262), then the raw rows into their slots, skipping
+//                          slots >= cap (kernels.py:265-268), so an overflow is seen from
+//                          the counter.
+// The append path (cache.py:100-112) runs a write (+ page encode), a one-workgroup slot
+// scan and a raw-row copy with the token count read from device memory, so a decode step
+// can be captured in a HIP graph.
 #include "tile.hpp"
 #include "../../include/exactkv.h"
 

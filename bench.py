@@ -615,6 +615,12 @@ def c3_stress(a):
                                     max(a.steps, 50), a.warmup, a.copies)
     alg = algorithmic_bytes([kcs[0], vcs[0]], B, TS, Hq, Hkv, lens)
     gbps = alg / (ms_split * 1e-3) / 1e9
+    # the page decoder (compressed -> bf16, the path decode_to_bf16 / decode_reference use):
+    # every byte of a key cache read once, the bf16 tensor written once
+    ms_dec = time_loop(lambda i: kernels.decode_to_bf16(kcs[i], TS), a.steps, a.warmup, a.copies)
+    c0 = kcs[0]
+    dec_bytes = (sum(getattr(c0, f).nbytes for f in ("sm", "code", "base", "rowmask", "rowoff"))
+                 + int(c0.cnt.item()) * 256 + B * TS * Hkv * 128 * 2)
     res = {
         "metric": "c3 decode-attn us with per-sequence lengths; encoder GB/s", "value": round(ms_c * 1e3, 2),
         "unit": "us", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_c, 5),
@@ -629,6 +635,7 @@ def c3_stress(a):
         "bf16_twin_us": round(ms_b * 1e3, 2), "speedup_vs_bf16": round(ms_b / ms_c, 3),
         "bit_identical_to_bf16": bool(identical), "pool_grows_in_prefill": grows[0],
         "raw_rows": int(kcs[0].cnt.item()) + int(vcs[0].cnt.item()), "encoder_GBps": enc,
+        "decoder_GBps": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1),
         "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(res), flush=True)

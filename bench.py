@@ -233,8 +233,11 @@ def cpu_baseline(kc, vc, q, B, T, runs, lens=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 400 for the attention shapes, 50 for the other workloads)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default: 200 for the attention shapes, 10 otherwise); a short "
+                         "warmup leaves the GPU below its steady clocks, which shows as +1-3 us per call")
     ap.add_argument("--workload", default="c2a",
                     choices=sorted(WORKLOADS) + ["c3", "e2e", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"])
     ap.add_argument("--e2e-prompt", type=int, default=4096)
@@ -253,6 +256,11 @@ def main():
                          "then a few launches of each attention kernel (with --workload c3: of the encoder "
                          "over the prefill's keys); no timing")
     a = ap.parse_args()
+    attn = a.workload in WORKLOADS or a.workload in ("c3", "c2a_paged")
+    if a.steps is None:
+        a.steps = 400 if attn else 50
+    if a.warmup is None:
+        a.warmup = 200 if attn else 10
     if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"):
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)

@@ -536,7 +536,7 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
         return (int64_t)b * a.Hq + (int64_t)(hb * a.HW + i / gh) * a.G + hg * 16 + i % gh;
     };
     if (ng > 1) {                                      // level 1: the group into its first split slot
-        for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {
+        for (int i = threadIdx.x >> 6; i < rows; i += blockDim.x >> 6) {
             const int64_t row = row_of(i);
             const RowMerge r = merge_row_dev(a, row, g0, 1, gn, lane);
             float* po = a.part_o + (row * a.nsplit + g0) * kD + 2 * lane;
@@ -550,147 +550,65 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
         if (!arrive_last(cnt + ng, ng)) return;
     }
     const int step = ng > 1 ? G1 : 1, n2 = ng > 1 ? ng : a.nsplit;
-    for (int i = threadIdx.x >> 6; i < rows; i += kWaves) {    // level 2: the groups (or splits) into the output
+    for (int i = threadIdx.x >> 6; i < rows; i += blockDim.x >> 6) {   // level 2: the groups (or splits) into the output
         const int64_t row = row_of(i);
         const RowMerge r = merge_row_dev(a, row, 0, step, n2, lane);
         reinterpret_cast<uint32_t*>(a.out + row * kD)[lane] = pack_bf16x2(r.n0 / r.den, r.n1 / r.den);
     }
 }
 
-template <bool COMP>
-__global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<COMP>::bytes];
-    __shared__ int progress[kWaves];                   // pages done per wavefront (priority hint)
-    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // uniform: scalar addressing
-    // workgroup: sequence b, token split, block of HW KV heads (all read the same tokens, so
-    // the workgroup's loads cover whole token rows of the [B, T, H, D] arrays); wavefront:
-    // head slot w % HW, page phase w / HW
-    const int split = blockIdx.x;
+// ---- pieces shared by the two split kernels
+
+// Phase merge through LDS: rows of 128 channels padded to kMoRow floats, so that the 16
+// heads of one write land in different banks (a 512-byte row stride put them all in the
+// same ones); both rings hold it.
+constexpr int kMoRow = kD + 4;
+constexpr int kMoBytes = (kWaves * 16 * kMoRow + 2 * kWaves * 16) * 4;
+static_assert(Ring<true>::bytes >= kMoBytes && Ring<false>::bytes >= kMoBytes, "phase merge must fit the ring");
+
+// Workgroup coordinates of a split-kernel launch: sequence b, token split, block hb of HW
+// KV heads, group hg of 16 query heads (gh of them real); the split's tokens [start, end)
+// (pages p0 .. pend - 1) and the window's first token wlo. Page phase ph (wavefronts ph*HW
+// .. ph*HW + HW - 1) takes pages p0 + ph + nphase * j, j < npw(ph).
+struct SplitCoords {
+    int split, hg, hb, b, hw_sh, nphase, wlo, start, end, NP, p0, pend, gh;
+    __device__ int npw(int ph) const { return pend - p0 > ph ? (pend - p0 - ph + nphase - 1) / nphase : 0; }
+};
+__device__ inline SplitCoords split_coords(const AttnArgs& a) {
+    SplitCoords c;
+    c.split = blockIdx.x;
     int y = blockIdx.y;
-    const int hg = y % a.HG;
+    c.hg = y % a.HG;
     y /= a.HG;
     const int nhb = a.Hkv / a.HW;
-    const int hb = y % nhb;
-    const int b = y / nhb;
-    const int hk = hb * a.HW + wave % a.HW;
-    const int phase = wave / a.HW, nphase = kWaves / a.HW;
-    int len = a.lens ? a.lens[b * a.lens_stride] : a.T;
+    c.hb = y % nhb;
+    c.b = y / nhb;
+    c.hw_sh = __builtin_ctz(a.HW);                    // HW = gcd(Hkv, 8), a power of two
+    c.nphase = kWaves >> c.hw_sh;
+    int len = a.lens ? a.lens[c.b * a.lens_stride] : a.T;
     len = min(max(len, 0), a.TS);
-    // sliding window: tokens [lo, len) only; the splits start at lo's page
-    const int wlo = a.window > 0 ? max(len - a.window, 0) : 0;
-    const int start = (wlo & ~(kPage - 1)) + split * a.split_len;
-    const int end = min(start + a.split_len, len);
-    const int NP = a.TS / kPage;
+    // sliding window: tokens [wlo, len) only; the splits start at wlo's page
+    c.wlo = a.window > 0 ? max(len - a.window, 0) : 0;
+    c.start = (c.wlo & ~(kPage - 1)) + c.split * a.split_len;
+    c.end = min(c.start + a.split_len, len);
+    c.NP = a.TS / kPage;
+    c.p0 = c.start / kPage;
+    c.pend = c.end > c.start ? (c.end + kPage - 1) / kPage : c.p0;
+    c.gh = min(16, a.G - c.hg * 16);
+    return c;
+}
 
-    float m_i = -INFINITY, l_i = 0.f;
-    f32x4 acc[8];
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+// Array page of page lp of sequence b: contiguous, or pool page block_table[b * bt_stride +
+// lp] clamped to the pool (a bad entry cannot read out of bounds). e: that table entry.
+__device__ inline int64_t array_page(const AttnArgs& a, const SplitCoords& c, int lp, int32_t e) {
+    if (a.block_table == nullptr) return (int64_t)c.b * c.NP + lp;
+    return (int64_t)min((uint32_t)e, (uint32_t)(a.pool_pages - 1));
+}
 
-    // this wavefront's pages: p0 + phase + nphase * j, j < npw
-    constexpr int NST = Ring<COMP>::nst;
-    constexpr int STB = Ring<COMP>::stage;
-    const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<COMP>::per_wave);   // this wave's (uniform)
-    const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
-    const LdsLane lo = lds_lane_offsets(r, g);
-    const int p0 = start / kPage;
-    const int pend = end > start ? (end + kPage - 1) / kPage : p0;
-    const int npw = pend - p0 > phase ? (pend - p0 - phase + nphase - 1) / nphase : 0;
-    const int64_t rs = a.Hkv;
-    const DmaLane dl = dma_lane_offsets<COMP>(lane, rs);
-    const PairSrc basep = pair_src((uint64_t)(uintptr_t)a.k.base, (uint64_t)(uintptr_t)a.v.base);
-    const PairSrc rawp = pair_src((uint64_t)(uintptr_t)a.k.raw, (uint64_t)(uintptr_t)a.v.raw);
-    const PairSrc rawn = pair_src((uint64_t)a.k.raw_rows, (uint64_t)a.v.raw_rows);
-
-    // rowmask / rowoff of the wavefront's pages. Lane i holds page i's (i < 64): loaded once,
-    // with q, by direct-to-LDS loads, then read into VGPRs, so that a page's values are
-    // v_readlane of its index. Scalar loads inside the loop would cost more: SMEM and LDS
-    // share lgkmcnt and SMEM returns out of order, so every wait for an LDS read there would
-    // also wait for the scalar loads in flight. Scalar loads serve the first two pages (their
-    // raw rows go out with the first DMA) and pages past 64.
-    // Page index (in the arrays) of the wavefront's page j: contiguous, or through the block
-    // table, whose entries for the wavefront's pages are read once into VGPRs (lane i: page
-    // i, i < 64) like the page table below.
-    int32_t vbt = 0;
-    auto gpage = [&](int j) -> int64_t {
-        const int lp = p0 + phase + nphase * j;
-        if (a.block_table == nullptr) return (int64_t)b * NP + lp;
-        const int32_t e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(a.block_table + b * a.bt_stride + lp);
-        return (int64_t)min((uint32_t)e, (uint32_t)(a.pool_pages - 1));     // a bad entry cannot read out of bounds
-    };
-    auto meta_s = [&](int j) {
-        PageMeta m{0u, 0u, 0, 0};
-        if constexpr (COMP) {
-            const int64_t page = gpage(j) * rs + hk;
-            m.mk = (uint32_t)const_ld(a.k.rowmask + page);
-            m.ok = const_ld(a.k.rowoff + page);
-            m.mv = (uint32_t)const_ld(a.v.rowmask + page);
-            m.ov = const_ld(a.v.rowoff + page);
-        }
-        return m;
-    };
-    uint32_t vmk = 0u, vmv = 0u;
-    int32_t vok = 0, vov = 0;
-    auto meta = [&](int j) {
-        if (j >= 64) return meta_s(j);
-        return PageMeta{(uint32_t)__builtin_amdgcn_readlane((int)vmk, j), (uint32_t)__builtin_amdgcn_readlane((int)vmv, j),
-                        __builtin_amdgcn_readlane(vok, j), __builtin_amdgcn_readlane(vov, j)};
-    };
-    auto issue_bytes = [&](int j, uint32_t sb) {
-        const int64_t gp = gpage(j);
-        dma_page_bytes<COMP>(a, dl, gp * kPage * rs + hk, gp * rs + hk, sb, lane, basep);
-    };
-    auto issue_raw = [&](int j, const PageMeta& m) {
-        if constexpr (COMP) dma_page_raw(lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), rawp, rawn);
-    };
-    auto issue = [&](int j, uint32_t sb, const PageMeta& m) {
-        issue_bytes(j, sb);
-        issue_raw(j, m);
-    };
-    // q through the last stage, which no page uses before page NST - 1 is issued
-    const int gh = min(16, a.G - hg * 16);
-    const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
-    const uint32_t mst = qst + 4096u;                  // rowmask K | rowoff K | rowmask V | rowoff V
-    if (a.block_table != nullptr) {                    // the block-table entries first: every address needs them
-        const uint32_t bst = mst + 1024u;
-        const int lp = p0 + phase + nphase * min(lane, max(npw - 1, 0));
-        dma4(a.block_table + b * a.bt_stride + min(lp, (int)(a.TS / kPage) - 1), bst);
-        wait_vm<0>();
-        vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    q_dma(a, b, hk, hg, gh, lane, qst);
-    if constexpr (COMP) {
-        const int i = min(lane, max(npw - 1, 0));     // per lane: the wavefront's page i
-        const int64_t gp = a.block_table == nullptr ? (int64_t)b * NP + min(p0 + phase + nphase * i, NP - 1)
-                                                    : (int64_t)min((uint32_t)vbt, (uint32_t)(a.pool_pages - 1));
-        const int64_t page = gp * rs + hk;
-        dma4(a.k.rowmask + page, mst);
-        dma4(a.k.rowoff + page, mst + 256u);
-        dma4(a.v.rowmask + page, mst + 512u);
-        dma4(a.v.rowoff + page, mst + 768u);
-    }
-    // The first page's bytes go out before its metadata is known; its raw-row load follows
-    // once the page table has landed. The compressed kernel issues the second page only
-    // then: every wavefront's first burst is issued at once at the start, and its DMAs stall
-    // at issue while the CU's memory pipeline is full, so a shorter first burst gets each
-    // wavefront's first page in sooner (issue done at a median 1.9 instead of 3.7 us at c2a).
-    if (npw > 0) issue_bytes(0, ring);
-    if (!COMP && NST == 3 && npw > 1) issue_bytes(1, ring + STB);
-    // q and the page table have landed once only the first pages' byte loads are in flight
-    constexpr int kBytesPerPage = COMP ? kDmaPerPage[1] - 1 : kDmaPerPage[0];
-    const int first = COMP ? min(npw, 1) : min(npw, NST - 1);
-    if (first >= 2)
-        wait_vm<2 * kBytesPerPage>();
-    else if (first == 1)
-        wait_vm<kBytesPerPage>();
-    else
-        wait_vm<0>();
-    // Q^T as the B operand: column = head hg*16 + r of this KV head's group, k-block kc
-    // holds channels 16g + 8kc.. (kc < 2) or 64 + 16g + 8(kc-2).. (kc >= 2); heads past
-    // the group are zero.
-    bf16x8 qop[4];
+// Q^T as the B operand of the score MFMAs, from q staged at qst (head h at qst + 256 h):
+// column = head hg*16 + r of this KV head's group, k-block kc holds channels 16g + 8kc..
+// (kc < 2) or 64 + 16g + 8(kc-2).. (kc >= 2); heads past the group are zero.
+__device__ inline void load_qop(uint32_t qst, int r, int g, int gh, bf16x8 (&qop)[4]) {
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
         const int d0 = kc < 2 ? 16 * g + 8 * kc : 64 + 16 * g + 8 * (kc - 2);
@@ -701,191 +619,108 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
         // before every page's score MFMAs instead of keeping the result
         asm volatile("" : "+v"(qop[kc]));
     }
-    if constexpr (COMP) {
-        vmk = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 4u * lane));
-        vok = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 256u + 4u * lane));
-        vmv = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 512u + 4u * lane));
-        vov = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 768u + 4u * lane));
+}
+
+// Score MFMAs of one page: S^T = K Q^T (tokens = rows, the group's query heads = columns)
+__device__ inline f32x4 page_scores(const uint32_t (&kd)[16], const bf16x8 (&qop)[4]) {
+    f32x4 sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+        sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]),
+                                                     qop[kc], sa, 0, 0, 0);
+    return sa;
+}
+
+// V^T operands of the P.V MFMAs out of the page's bf16 V tile (at sb + toff)
+__device__ inline void read_vt(uint32_t sb, const LdsLane& lo, int toff, s16x4 (&vt)[8]) {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        const lds_u8* tp = lds_ptr(sb + lo.tr[nb & 3]) + toff + (nb >= 4 ? 128 : 0);
+        vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)tp);
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers before their stage is reused
-    if constexpr (COMP) {
-        if (npw > 0) issue_raw(0, meta(0));
-        if (npw > 1) issue_bytes(1, ring + STB);
-        if (npw > 1) issue_raw(1, meta(1));
+}
+
+// Rows of a ragged page (past the split's end or before the window) read as zero
+__device__ inline void zero_invalid_rows(bool valid, uint32_t (&d)[16]) {
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d[i] = 0u;
     }
+}
 
-    progress[wave] = 0;
-    int stg = 0;                                       // stage of page j (j % NST)
-    for (int j = 0; j < npw; ++j) {
-        // stage j is complete once only page j + 1's loads are in flight (its bytes, then its
-        // raw-row load, issued after page j's raw-row load -- in the prologue too)
-        if (NST == 3 && j + 1 < npw) {
-            if constexpr (COMP) {
-                const int next = raw_loads(meta(j + 1));
-                wait_vm_n(kDmaPerPage[1] - 1 + next);
-            } else {
-                wait_vm<kDmaPerPage[COMP]>();
-            }
-        } else {
-            wait_vm<0>();
-        }
-        const uint32_t sb = ring + (uint32_t)(stg * STB);
-        const int stn = stg == 0 ? NST - 1 : stg - 1;  // stage of page j + NST - 1
-        stg = stg == NST - 1 ? 0 : stg + 1;
-        const int pg = p0 + phase + nphase * j;
-        const int t0 = pg * kPage;
-        const bool ragged = t0 + kPage > end || t0 < wlo;  // uniform: a split's last page, or the window's first
-        auto row_valid = [&]() { return t0 + r < end && t0 + r >= wlo; };
-        const PageMeta mc = COMP ? meta(j) : PageMeta{0u, 0u, 0, 0};
-
-        // The next page's byte loads go out at once, into the stage the previous page used
-        // (its last LDS reads are waited for first). The compressed page's raw-row load
-        // follows once this page's raw rows are out of their slot, which it reuses; the
-        // waits above count both.
-        const PageMeta mn = COMP && j + NST - 1 < npw ? meta(j + NST - 1) : PageMeta{0u, 0u, 0, 0};
-        if (j + NST - 1 < npw) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue_bytes(j + NST - 1, ring + (uint32_t)(stn * STB));
-        }
-        // Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one, and
-        // the older one's first loads are also served first: left alone it runs ahead and its
-        // partner finishes last. The one that is behind takes the higher priority. The
-        // partner's count is read here (an unsynchronised hint: either value is fine) and
-        // used once the page's LDS reads are out, so its round trip overlaps theirs.
-        const int other = progress[wave ^ 4];
-        progress[wave] = j;
-        auto set_priority = [&]() {
-            if (j > 0) {
-                if (j < other)
-                    __builtin_amdgcn_s_setprio(2);
-                else
-                    __builtin_amdgcn_s_setprio(0);
-            }
-        };
-
-        // ---- K and V bytes out of the stage together; the V reads overlap the K rebuild
-        uint32_t kd[16], vd[16];
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (COMP) {
-            PageBytes pk, pv;
-            stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
-            stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
-            set_priority();
-            const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
-            rebuild_values(pk, kd);
-            if (mc.mk != 0) {                          // page with raw K rows
-                keep_branch();
-                splice_raw<false>(a, mc, slot, r, g, kd);
-            }
-            if (ragged) {                              // rows past the end of the split: zero
-                keep_branch();
-                if (!row_valid()) {
+// One page's online softmax and P.V, the same code in both kernels (so that their results
+// agree bit for bit). Lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
+// max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into the
+// exponent's fma: p = 2^(s * scale - m). Tokens outside the split or the window score
+// -inf; only a ragged page has any. p is rounded to bf16 for P.V, l sums the fp32 p.
+__device__ __forceinline__ void page_softmax_pv(f32x4 sa, const s16x4 (&vt)[8], bool ragged, int t0, int end, int wlo,
+                                                int g, float qk_scale, float& m_i, float& l_i, f32x4 (&acc)[8]) {
+    // The score MFMAs' result is read below after branches whose opaque asm the compiler's
+    // hazard tracking has counted as wait states (reads then saw stale accumulators). Pass
+    // it through 16 explicit wait states instead: the asm defines sa, so every later read
+    // follows it.
+    asm volatile("s_nop 7\n\ts_nop 7" : "+v"(sa));
+    float sc[4] = {sa[0], sa[1], sa[2], sa[3]};
+    if (ragged) {
+        keep_branch();
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) kd[i] = 0u;
-                }
-            }
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc)
-                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
-            // V rebuild while the score MFMAs run; the tile overwrites the K bytes (read above)
-            rebuild_values(pv, vd);
-            if (mc.mv != 0) {
-                keep_branch();
-                splice_raw<true>(a, mc, slot, r, g, vd);
-            }
-            if (ragged) {
-                keep_branch();
-                if (!row_valid()) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) vd[i] = 0u;
-                }
-            }
-            if (j + NST - 1 < npw) issue_raw(j + NST - 1, mn);   // this page's raw rows are out of the slot
-            write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
-        } else {
-            stage_bf16_k(sb, lo, kd);
-            set_priority();
-            if (ragged) {
-                keep_branch();
-                if (!row_valid()) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) kd[i] = 0u;
-                }
-            }
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc)
-                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
-            if (ragged) {                              // ragged last page: zero the V rows past the end
-                keep_branch();
-                if (!row_valid()) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) vd[i] = 0u;
-                    write_v_tile(sb, lo, Ring<COMP>::vtile, vd);
-                }
-            }
-        }
-
-        // V^T operands of this page's P.V MFMAs out of the V tile now (the tile's writes come
-        // first in the wavefront's LDS order), so their latency overlaps the softmax below.
-        s16x4 vt[8];
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-            const lds_u8* tp = lds_ptr(sb + lo.tr[nb & 3]) + Ring<COMP>::vtile + (nb >= 4 ? 128 : 0);
-            vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)tp);
-        }
-        // The score MFMAs' result is read below after the branches above, whose opaque asm the
-        // compiler's hazard tracking has counted as wait states (reads then saw stale
-        // accumulators). Pass it through 16 explicit wait states instead: the asm defines sa,
-        // so every later read follows it.
-        asm volatile("s_nop 7\n\ts_nop 7" : "+v"(sa));
-        // ---- online softmax: lane = head r, tokens t0 + 4g + i; m_i in scaled (log2) units.
-        // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into
-        // the exponent's fma: p = 2^(s * scale - m). Tokens outside the split or the window
-        // score -inf; only a ragged page has any (its branch follows the explicit wait
-        // states above, so the reads inside cannot see the accumulators early).
-        float sc[4] = {sa[0], sa[1], sa[2], sa[3]};
-        if (ragged) {
-            keep_branch();
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (t0 + 4 * g + i >= end || t0 + 4 * g + i < wlo) sc[i] = -INFINITY;
-        }
-        float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mloc = group_max(mloc) * a.qk_scale;
-        const float m_new = fmaxf(m_i, mloc);
-        const float alpha = fast_exp2(m_i - m_new);
-        float psum = 0.f;
-        bf16x4 pb4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(__builtin_fmaf(sc[i], a.qk_scale, -m_new));
-            psum += p;
-            pb4[i] = (__bf16)p;
-        }
-        l_i = l_i * alpha + psum;
-        m_i = m_new;
-        if (__ballot(alpha != 1.f) != 0) {             // rescale only when some head's max moved
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
-        }
-
-        // ---- O^T += V^T P^T: V^T rows 4g..4g+3 of channel 16nb + r via the transpose read
-        const s16x4 pop = __builtin_bit_cast(s16x4, pb4);
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[nb], pop, acc[nb], 0, 0, 0);
+        for (int i = 0; i < 4; ++i)
+            if (t0 + 4 * g + i >= end || t0 + 4 * g + i < wlo) sc[i] = -INFINITY;
     }
+    float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mloc = group_max(mloc) * qk_scale;
+    const float m_new = fmaxf(m_i, mloc);
+    const float alpha = fast_exp2(m_i - m_new);
+    float psum = 0.f;
+    bf16x4 pb4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(__builtin_fmaf(sc[i], qk_scale, -m_new));
+        psum += p;
+        pb4[i] = (__bf16)p;
+    }
+    l_i = l_i * alpha + psum;
+    m_i = m_new;
+    if (__ballot(alpha != 1.f) != 0) {                 // rescale only when some head's max moved
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
+    }
+    // O^T += V^T P^T: V^T rows 4g..4g+3 of channel 16nb + r; the C layout of S^T is exactly
+    // the P^T operand layout, and O^T accumulates with lane = head
+    const s16x4 pop = __builtin_bit_cast(s16x4, pb4);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[nb], pop, acc[nb], 0, 0, 0);
+}
 
-    // ---- merge the page phases of each head (same algebra as the split merge)
+// Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one: left
+// alone it runs ahead and its partner finishes last. The one that is behind takes the
+// higher priority (the partner's page count is an unsynchronised hint: either value is
+// fine).
+__device__ inline void balance_priority(int j, int other) {
+    if (j > 0) {
+        if (j < other)
+            __builtin_amdgcn_s_setprio(2);
+        else
+            __builtin_amdgcn_s_setprio(0);
+    }
+}
+
+// After the page loop: the page phases of each head merged through LDS (same algebra as the
+// split merge) into one partial per (split, query head), then the fused merge when asked
+// for. Every wavefront of the workgroup calls it (its barriers count them all); those with
+// active == false (loader wavefronts) contribute no partial. lds: the workgroup's ring
+// (at least kMoBytes), free by now.
+__device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoords& c, uint8_t* lds, int wave,
+                                               int lane, bool active, int hk, const f32x4 (&acc)[8], float m_i,
+                                               float l_i) {
+    const int r = lane & 15, g = lane >> 4;
     // the accumulators were last written by MFMAs, possibly across inline assembly that the
     // hazard tracking may count as wait states: pad explicitly before the first reads
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     const float l_t = group_sum(l_i);
-    const int64_t hq0 = (int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16;     // first query head of this wave
-    if (nphase == 1) {                                 // one wavefront per head: write its partial
-        if (r < gh) {
-            const int64_t prow = (hq0 + r) * a.nsplit + split;
+    if (c.nphase == 1) {                               // one wavefront per head: write its partial
+        if (active && r < c.gh) {
+            const int64_t prow = ((int64_t)c.b * a.Hq + (int64_t)hk * a.G + c.hg * 16 + r) * a.nsplit + c.split;
             if (a.counters == nullptr) {
 #pragma unroll
                 for (int nb = 0; nb < 8; ++nb)
@@ -903,42 +738,45 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
                 }
             }
         }
-        merge_tail(a, b, hb, hg, gh, split);
+        merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
         return;
     }
     __syncthreads();
-    float* mo = reinterpret_cast<float*>(lds);            // [wave][16 heads][128]
-    float* mm = mo + kWaves * 16 * kD;                     // [wave][16]
+    float* mo = reinterpret_cast<float*>(lds);            // [wave][16 heads][kMoRow]
+    float* mm = mo + kWaves * 16 * kMoRow;                 // [wave][16]
     float* ml = mm + kWaves * 16;
+    if (active) {
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-        *reinterpret_cast<f32x4*>(mo + (wave * 16 + r) * kD + 16 * nb + 4 * g) = acc[nb];
-    if (g == 0) {
-        mm[wave * 16 + r] = m_i;
-        ml[wave * 16 + r] = l_t;
+        for (int nb = 0; nb < 8; ++nb)
+            *reinterpret_cast<f32x4*>(mo + (wave * 16 + r) * kMoRow + 16 * nb + 4 * g) = acc[nb];
+        if (g == 0) {
+            mm[wave * 16 + r] = m_i;
+            ml[wave * 16 + r] = l_t;
+        }
     }
     __syncthreads();
     // thread t merges (head slot, head, 4-channel group) items, four channels with the same
     // per-channel arithmetic as one; waves of one head slot s are s, s + HW, ...
-    for (int idx = threadIdx.x; idx < a.HW * gh * (kD / 4); idx += kThreads) {
+    for (int idx = threadIdx.x; idx < a.HW * c.gh * (kD / 4); idx += blockDim.x) {
         const int d = 4 * (idx & (kD / 4 - 1));
-        const int h = (idx >> 5) % gh;
-        const int hs = (idx >> 5) / gh;
+        const int h = (idx >> 5) % c.gh;
+        const int hs = (idx >> 5) / c.gh;
         float M = -INFINITY;
-        for (int ph = 0; ph < nphase; ++ph) M = fmaxf(M, mm[(ph * a.HW + hs) * 16 + h]);
+        for (int ph = 0; ph < c.nphase; ++ph) M = fmaxf(M, mm[(ph * a.HW + hs) * 16 + h]);
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
         float l = 0.f;
         if (M != -INFINITY) {
-            for (int ph = 0; ph < nphase; ++ph) {
+            for (int ph = 0; ph < c.nphase; ++ph) {
                 const int w = ph * a.HW + hs;
                 const float wt = fast_exp2(mm[w * 16 + h] - M);
-                const f32x4 v = *reinterpret_cast<const f32x4*>(mo + (w * 16 + h) * kD + d);
+                const f32x4 v = *reinterpret_cast<const f32x4*>(mo + (w * 16 + h) * kMoRow + d);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) o[c] += wt * v[c];
+                for (int k = 0; k < 4; ++k) o[k] += wt * v[k];
                 l += wt * ml[w * 16 + h];
             }
         }
-        const int64_t prow = ((int64_t)b * a.Hq + (int64_t)(hb * a.HW + hs) * a.G + hg * 16 + h) * a.nsplit + split;
+        const int64_t prow =
+            ((int64_t)c.b * a.Hq + (int64_t)(c.hb * a.HW + hs) * a.G + c.hg * 16 + h) * a.nsplit + c.split;
         if (a.counters == nullptr) {
             *reinterpret_cast<f32x4*>(a.part_o + prow * kD + d) = o;
             if (d == 0) {
@@ -953,7 +791,348 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel(AttnArgs a) {
             }
         }
     }
-    merge_tail(a, b, hb, hg, gh, split);
+    merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
+}
+
+template <bool COMP>
+__global__ void attn_split_kernel(AttnArgs a);
+
+// ---- compressed split kernel: 8 compute wavefronts (head slots x page phases) and
+// kLoaders loader wavefronts.
+//
+// Loader l issues every byte load of the pages of compute wavefronts kWpl*l .. kWpl*l +
+// kWpl - 1 into their rings, in rounds (page j of each of them, in order), keeps kLoadAhead
+// + 1 pages in flight, and publishes a page (ready[w] = pages of w landed) once its loads
+// are complete (its own s_waitcnt vmcnt: loads complete in order). It issues page j of w
+// only once avail[w] > j, i.e. once w has handed back the stage that page j reuses. A
+// compute wavefront waits for ready[w] > j, reads the page, and hands the stage back as
+// soon as its last LDS read of it has returned. So the compute wavefronts never stall on a
+// full memory pipeline (the loaders do), and the CU's loads stay in flight while they
+// compute. The flags live in LDS; every wait on them is bounded (kSpinMax).
+constexpr int kLoaders = 2;
+constexpr int kWpl = kWaves / kLoaders;          // compute wavefronts per loader
+constexpr int kCompThreads = 64 * (kWaves + kLoaders);
+constexpr int kLoadAhead = 3;                    // pages a loader keeps in flight besides the newest
+constexpr int kBytesLoads = kDmaPerPage[1] - 1;  // byte loads per compressed page
+constexpr int kSpinMax = 1 << 22;                // bound of every flag wait (a correct run never reaches it)
+static_assert((kLoadAhead + 1) * kBytesLoads <= 63, "a loader's loads in flight must fit vmcnt");
+
+__device__ inline int lds_flag_ld(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ inline void lds_flag_st(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+
+// Loader wavefront l (see above)
+__device__ __forceinline__ void comp_loader(const AttnArgs& a, const SplitCoords& c, uint32_t lds0, int* ready,
+                                            const int* avail, int l, int lane) {
+    constexpr int NST = Ring<true>::nst, STB = Ring<true>::stage;
+    __builtin_amdgcn_s_setprio(3);                     // issue as soon as the memory pipeline takes it
+    const int64_t rs = a.Hkv;
+    const DmaLane dl = dma_lane_offsets<true>(lane, rs);
+    const PairSrc basep = pair_src((uint64_t)(uintptr_t)a.k.base, (uint64_t)(uintptr_t)a.v.base);
+    const int w0 = kWpl * l;
+    auto lpage = [&](int i, int j) { return c.p0 + ((w0 + i) >> c.hw_sh) + c.nphase * j; };
+    const int jmax = c.npw(w0 >> c.hw_sh);             // wavefront w0 has the lowest phase: the most pages
+    // paged: the block-table entries of pages p0 .. p0 + 63 (lane k: page p0 + k), read once
+    int32_t vbt = 0;
+    if (a.block_table != nullptr) {
+        vbt = a.block_table[c.b * a.bt_stride + min(c.p0 + lane, c.NP - 1)];
+        asm volatile("" : "+v"(vbt));                  // waited for here, once, before any page load
+    }
+    int inflight = 0, pi = 0, pj = 0;                  // the oldest page in flight: wavefront w0 + pi, page pj
+    auto publish = [&]() {
+        lds_flag_st(&ready[w0 + pi], pj + 1);
+        do {
+            if (++pi == kWpl) {
+                pi = 0;
+                ++pj;
+            }
+        } while (pj < jmax && lpage(pi, pj) >= c.pend);
+        --inflight;
+    };
+    for (int j = 0; j < jmax; ++j) {
+        for (int i = 0; i < kWpl; ++i) {
+            const int lp = lpage(i, j);
+            if (lp >= c.pend) continue;
+            const int w = w0 + i;
+            if (lds_flag_ld(&avail[w]) <= j) {         // its stage is still in use: publish all, then wait
+                wait_vm<0>();
+                while (inflight > 0) publish();
+                for (int s = 0; s < kSpinMax && lds_flag_ld(&avail[w]) <= j; ++s) __builtin_amdgcn_s_sleep(1);
+            }
+            int32_t e = 0;
+            if (a.block_table != nullptr)
+                e = lp - c.p0 < 64 ? __builtin_amdgcn_readlane(vbt, lp - c.p0)
+                                   : const_ld(a.block_table + c.b * a.bt_stride + lp);
+            const int64_t gp = array_page(a, c, lp, e);
+            const int hk = c.hb * a.HW + (w & (a.HW - 1));
+            const uint32_t sb = lds0 + (uint32_t)(w * Ring<true>::per_wave + (j % NST) * STB);
+            dma_page_bytes<true>(a, dl, gp * kPage * rs + hk, gp * rs + hk, sb, lane, basep);
+            if (++inflight > kLoadAhead) {
+                wait_vm<kLoadAhead * kBytesLoads>();
+                publish();
+            }
+        }
+    }
+    wait_vm<0>();
+    while (inflight > 0) publish();
+}
+
+template <>
+__global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs a) {
+    constexpr int NST = Ring<true>::nst, STB = Ring<true>::stage;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<true>::bytes];
+    __shared__ int progress[kWaves];                   // pages done per compute wavefront (priority hint)
+    __shared__ int ready[kWaves];                      // pages of wavefront w in its ring (loader -> w)
+    __shared__ int avail[kWaves];                      // pages of w its loader may issue (w -> loader)
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // uniform: scalar addressing
+    const SplitCoords c = split_coords(a);
+    const int hk = c.hb * a.HW + (wave & (a.HW - 1));
+    if (threadIdx.x < kWaves) {
+        ready[threadIdx.x] = 0;
+        avail[threadIdx.x] = NST - 1;                  // the last stage holds q and the page table at first
+    }
+    __syncthreads();
+
+    float m_i = -INFINITY, l_i = 0.f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (wave >= kWaves) {
+        comp_loader(a, c, lds_addr(lds), ready, avail, wave - kWaves, lane);
+    } else {
+        const int phase = wave >> c.hw_sh;
+        const int npw = c.npw(phase);
+        const int64_t rs = a.Hkv;
+        const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<true>::per_wave);   // this wave's (uniform)
+        const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
+        const LdsLane lo = lds_lane_offsets(r, g);
+        const PairSrc rawp = pair_src((uint64_t)(uintptr_t)a.k.raw, (uint64_t)(uintptr_t)a.v.raw);
+        const PairSrc rawn = pair_src((uint64_t)a.k.raw_rows, (uint64_t)a.v.raw_rows);
+
+        // rowmask / rowoff of the wavefront's pages. Lane i holds page i's (i < 64): loaded
+        // once, with q, by direct-to-LDS loads, then read into VGPRs, so that a page's values
+        // are v_readlane of its index (scalar loads for pages past 64). The same for the
+        // block-table entries of the wavefront's pages (paged caches).
+        int32_t vbt = 0;
+        auto gpage = [&](int j) -> int64_t {
+            const int lp = c.p0 + phase + c.nphase * j;
+            int32_t e = 0;
+            if (a.block_table != nullptr)
+                e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(a.block_table + c.b * a.bt_stride + lp);
+            return array_page(a, c, lp, e);
+        };
+        auto meta_s = [&](int j) {
+            const int64_t page = gpage(j) * rs + hk;
+            return PageMeta{(uint32_t)const_ld(a.k.rowmask + page), (uint32_t)const_ld(a.v.rowmask + page),
+                            const_ld(a.k.rowoff + page), const_ld(a.v.rowoff + page)};
+        };
+        uint32_t vmk = 0u, vmv = 0u;
+        int32_t vok = 0, vov = 0;
+        auto meta = [&](int j) {
+            if (j >= 64) return meta_s(j);
+            return PageMeta{(uint32_t)__builtin_amdgcn_readlane((int)vmk, j),
+                            (uint32_t)__builtin_amdgcn_readlane((int)vmv, j), __builtin_amdgcn_readlane(vok, j),
+                            __builtin_amdgcn_readlane(vov, j)};
+        };
+        auto issue_raw = [&](int j, const PageMeta& m) {
+            dma_page_raw(lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), rawp, rawn);
+        };
+        // q and the page table through the last stage, which no page uses before the
+        // wavefront hands it over (avail = NST below)
+        const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
+        const uint32_t mst = qst + 4096u;              // rowmask K | rowoff K | rowmask V | rowoff V
+        const int i_pg = min(lane, max(npw - 1, 0));   // per lane: the wavefront's page i
+        if (a.block_table != nullptr) {                // the block-table entries first: every address needs them
+            const uint32_t bst = mst + 1024u;
+            dma4(a.block_table + c.b * a.bt_stride + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1), bst);
+            wait_vm<0>();
+            vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        q_dma(a, c.b, hk, c.hg, c.gh, lane, qst);
+        {
+            const int64_t gp = a.block_table == nullptr ? (int64_t)c.b * c.NP + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1)
+                                                        : array_page(a, c, 0, vbt);
+            const int64_t page = gp * rs + hk;
+            dma4(a.k.rowmask + page, mst);
+            dma4(a.k.rowoff + page, mst + 256u);
+            dma4(a.v.rowmask + page, mst + 512u);
+            dma4(a.v.rowoff + page, mst + 768u);
+        }
+        wait_vm<0>();
+        bf16x8 qop[4];
+        load_qop(qst, r, g, c.gh, qop);
+        vmk = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 4u * lane));
+        vok = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 256u + 4u * lane));
+        vmv = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mst + 512u + 4u * lane));
+        vov = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mst + 768u + 4u * lane));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers
+        lds_flag_st(&avail[wave], NST);
+        // raw rows of a page travel through the wavefront's two raw slots (page parity),
+        // issued two pages ahead by the wavefront itself
+        if (npw > 0) issue_raw(0, meta(0));
+        if (npw > 1) issue_raw(1, meta(1));
+
+        progress[wave] = 0;
+        int stg = 0;                                   // stage of page j (j % NST)
+        for (int j = 0; j < npw; ++j) {
+            // page j's raw rows have landed once only page j + 1's are in flight
+            if (j + 1 < npw)
+                wait_vm_n(raw_loads(meta(j + 1)));
+            else
+                wait_vm<0>();
+            if (lds_flag_ld(&ready[wave]) <= j) {      // page j's bytes: published by the loader
+                for (int s = 0; s < kSpinMax && lds_flag_ld(&ready[wave]) <= j; ++s) __builtin_amdgcn_s_sleep(0);
+            }
+            asm volatile("" ::: "memory");
+            const uint32_t sb = ring + (uint32_t)(stg * STB);
+            stg = stg == NST - 1 ? 0 : stg + 1;
+            const int t0 = (c.p0 + phase + c.nphase * j) * kPage;
+            const bool ragged = t0 + kPage > c.end || t0 < c.wlo;   // uniform: a split's last page, or the window's first
+            const bool valid = t0 + r < c.end && t0 + r >= c.wlo;
+            const PageMeta mc = meta(j);
+            const PageMeta mn = j + NST - 1 < npw ? meta(j + NST - 1) : PageMeta{0u, 0u, 0, 0};
+            const int other = progress[wave ^ 4];
+            progress[wave] = j;
+
+            // V first: its tile is written and its V^T operands read while K is rebuilt, so
+            // that the stage goes back to the loader right after the score MFMAs
+            PageBytes pk, pv;
+            stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
+            stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
+            balance_priority(j, other);
+            const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
+            uint32_t kd[16], vd[16];
+            rebuild_values(pv, vd);
+            if (mc.mv != 0) {                          // page with raw V rows
+                keep_branch();
+                splice_raw<true>(a, mc, slot, r, g, vd);
+            }
+            if (ragged) {
+                keep_branch();
+                zero_invalid_rows(valid, vd);
+            }
+            write_v_tile(sb, lo, Ring<true>::vtile, vd);     // over the K bytes, read above
+            s16x4 vt[8];
+            read_vt(sb, lo, Ring<true>::vtile, vt);
+            rebuild_values(pk, kd);
+            if (mc.mk != 0) {
+                keep_branch();
+                splice_raw<false>(a, mc, slot, r, g, kd);
+            }
+            if (ragged) {
+                keep_branch();
+                zero_invalid_rows(valid, kd);
+            }
+            const f32x4 sa = page_scores(kd, qop);
+            // this page's raw rows are out of their slot: page j + 2's go there
+            if (j + NST - 1 < npw) issue_raw(j + NST - 1, mn);
+            // every LDS read of the stage (bytes, V^T operands) has returned: hand it back
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_flag_st(&avail[wave], j + NST + 1);
+            page_softmax_pv(sa, vt, ragged, t0, c.end, c.wlo, g, a.qk_scale, m_i, l_i, acc);
+        }
+    }
+    split_epilogue(a, c, lds, wave, lane, wave < kWaves, hk, acc, m_i, l_i);
+}
+
+// ---- bf16 twin: 8 wavefronts, each issuing its own pages' loads into a 2-stage ring (one
+// page ahead); the same softmax / P.V code and epilogue as the compressed kernel.
+template <>
+__global__ void __launch_bounds__(kThreads) attn_split_kernel<false>(AttnArgs a) {
+    constexpr int NST = Ring<false>::nst, STB = Ring<false>::stage;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<false>::bytes];
+    __shared__ int progress[kWaves];
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const SplitCoords c = split_coords(a);
+    const int hk = c.hb * a.HW + (wave & (a.HW - 1));
+    const int phase = wave >> c.hw_sh;
+    const int npw = c.npw(phase);
+    const int64_t rs = a.Hkv;
+    float m_i = -INFINITY, l_i = 0.f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<false>::per_wave);
+    const LdsLane lo = lds_lane_offsets(r, g);
+    const DmaLane dl = dma_lane_offsets<false>(lane, rs);
+    const PairSrc nobase{0ull, 0ull};
+    int32_t vbt = 0;
+    auto gpage = [&](int j) -> int64_t {
+        const int lp = c.p0 + phase + c.nphase * j;
+        int32_t e = 0;
+        if (a.block_table != nullptr)
+            e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(a.block_table + c.b * a.bt_stride + lp);
+        return array_page(a, c, lp, e);
+    };
+    auto issue = [&](int j, uint32_t sb) {
+        const int64_t gp = gpage(j);
+        dma_page_bytes<false>(a, dl, gp * kPage * rs + hk, gp * rs + hk, sb, lane, nobase);
+    };
+    // q through the last stage, which no page uses before page NST - 1 is issued
+    const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
+    if (a.block_table != nullptr) {
+        const uint32_t bst = qst + 5120u;
+        const int i_pg = min(lane, max(npw - 1, 0));
+        dma4(a.block_table + c.b * a.bt_stride + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1), bst);
+        wait_vm<0>();
+        vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    q_dma(a, c.b, hk, c.hg, c.gh, lane, qst);
+    if (npw > 0) {
+        issue(0, ring);
+        wait_vm<kDmaPerPage[0]>();                     // q has landed once only page 0's loads are in flight
+    } else {
+        wait_vm<0>();
+    }
+    bf16x8 qop[4];
+    load_qop(qst, r, g, c.gh, qop);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q is in registers before its stage is reused
+
+    progress[wave] = 0;
+    int stg = 0;
+    for (int j = 0; j < npw; ++j) {
+        wait_vm<0>();                                  // page j has landed (the only page in flight)
+        const uint32_t sb = ring + (uint32_t)(stg * STB);
+        const int stn = stg == 0 ? NST - 1 : stg - 1;  // stage of page j + 1
+        stg = stg == NST - 1 ? 0 : stg + 1;
+        const int t0 = (c.p0 + phase + c.nphase * j) * kPage;
+        const bool ragged = t0 + kPage > c.end || t0 < c.wlo;
+        const bool valid = t0 + r < c.end && t0 + r >= c.wlo;
+        // the next page's loads go out at once, into the stage the previous page used (its
+        // last LDS reads are waited for first)
+        if (j + NST - 1 < npw) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(j + NST - 1, ring + (uint32_t)(stn * STB));
+        }
+        const int other = progress[wave ^ 4];
+        progress[wave] = j;
+        uint32_t kd[16];
+        stage_bf16_k(sb, lo, kd);
+        balance_priority(j, other);
+        if (ragged) {
+            keep_branch();
+            zero_invalid_rows(valid, kd);
+        }
+        const f32x4 sa = page_scores(kd, qop);
+        if (ragged) {                                  // ragged page: zero the staged V rows past the end
+            keep_branch();
+            if (!valid) {
+                uint32_t vd[16];
+                zero_invalid_rows(false, vd);
+                write_v_tile(sb, lo, Ring<false>::vtile, vd);
+            }
+        }
+        s16x4 vt[8];
+        read_vt(sb, lo, Ring<false>::vtile, vt);
+        page_softmax_pv(sa, vt, ragged, t0, c.end, c.wlo, g, a.qk_scale, m_i, l_i, acc);
+    }
+    split_epilogue(a, c, lds, wave, lane, true, hk, acc, m_i, l_i);
 }
 
 // Separate merge of up to 32 splits: one wavefront per (sequence, query head) row, every
@@ -1087,11 +1266,11 @@ static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
     t_split_start = t_split_stop = nullptr;
     if (e0 || e1) {
         if (comp)
-            hipExtLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kThreads), 0, stream, e0, e1, 0, a);
+            hipExtLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kCompThreads), 0, stream, e0, e1, 0, a);
         else
             hipExtLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kThreads), 0, stream, e0, e1, 0, a);
     } else if (comp) {
-        hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kCompThreads), 0, stream, a);
     } else {
         hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(kThreads), 0, stream, a);
     }

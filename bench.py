@@ -14,7 +14,7 @@ and the CPU baseline (the reference codec restated in PyTorch decoding both cach
 fp32 attention, on every host core this process may use; median of full calls).
 --workload cpu times that baseline at every benchmark shape without the GPU.
 
-    python bench.py [--steps 50] [--warmup 10] [--workload c2a]
+    python bench.py [--steps 400] [--warmup 200] [--workload c2a]
 """
 import argparse
 import json

@@ -4,30 +4,36 @@
 // _attn_block :46-59, _reduce_kernel :33-43.
 //
 // Grid: x = token split, y = (sequence, block of gcd(Hkv, 8) KV heads, group of 16 query
-// heads). A workgroup is 8 wavefronts (one workgroup per CU: it owns ~158 KB of LDS): each
-// KV head of the block gets 8 / gcd(Hkv, 8) of them ("page phases"), which take the split's
-// 16-token pages round robin, each with its own online-softmax state, and are merged
-// through LDS at the end (one partial per split and query head).
+// heads); one workgroup per CU (its LDS ring, ~158 KB). A workgroup has 8 compute
+// wavefronts: each KV head of the block gets 8 / gcd(Hkv, 8) of them ("page phases"),
+// which take the split's 16-token pages round robin, each with its own online-softmax
+// state, and are merged through LDS at the end (one partial per split and query head).
 //
-// Memory pipeline (per wavefront): each page is brought into a private LDS ring with a
-// fixed number (kDmaPerPage) of direct-to-LDS loads (global_load_lds_dwordx4/_dword), two
-// pages ahead for the compressed cache (3-stage ring) and one ahead for bf16 (2 stages).
-// The compiler does not order LDS reads after these loads, so every stage is read only
-// after an explicit s_waitcnt vmcnt(N) whose N counts the younger loads in flight. Rows
-// are placed with XOR swizzles chosen so that the later LDS reads are conflict-free.
+// Memory pipeline: every page is brought into its wavefront's private LDS ring by a fixed
+// number of direct-to-LDS loads (global_load_lds_dwordx4), rows placed with XOR swizzles
+// chosen so that the later LDS reads are conflict-free. The compiler does not order LDS
+// reads after these loads, so a stage is read only after an explicit s_waitcnt vmcnt(N)
+// of the wavefront that issued them.
+//   * Compressed cache: two more wavefronts per workgroup (loaders) issue every page's 7
+//     byte loads into the compute wavefronts' 3-stage rings and publish each landed page
+//     through an LDS flag; a compute wavefront waits for that flag and hands the stage
+//     back through another as soon as its last read of it has returned (see the kernel).
+//     Compute wavefronts never stall on a full memory pipeline; the loaders do.
+//   * bf16 twin: each wavefront issues its own pages' 8 loads, one page ahead (2 stages).
 //
 // Per page:
 //   * K and V are rebuilt bit-exactly in VGPRs from the staged bytes (tile.hpp), lane =
 //     token; raw rows are spliced in from the wavefront's raw-row slots, which one more
-//     direct-to-LDS load per page fills (issued once the page's metadata is known).
+//     direct-to-LDS load per page with raw rows fills (issued by the compute wavefront,
+//     which knows the page's metadata).
 //   * S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (tokens = rows, the G query heads of the
 //     KV head = columns, padded to 16); online softmax in base 2, scores scaled by
 //     D^-1/2 log2(e), p rounded to bf16 for P.V, l summed from fp32 p.
-//   * V goes back to LDS as a bf16 row tile (the compressed stage is consumed by then;
-//     the bf16 twin's stage already holds that tile), and ds_read_b64_tr_b16 reads it as
-//     the V^T operand of v_mfma_f32_16x16x16_bf16; the C layout of S^T is exactly the
-//     P^T operand layout, and O^T accumulates with lane = head, so the softmax rescale
-//     needs no cross-lane traffic.
+//   * V goes back to LDS as a bf16 row tile (over the compressed stage's K bytes, already
+//     in registers; the bf16 twin's stage holds that tile as loaded), and
+//     ds_read_b64_tr_b16 reads it as the V^T operand of v_mfma_f32_16x16x16_bf16; the C
+//     layout of S^T is exactly the P^T operand layout, and O^T accumulates with lane =
+//     head, so the softmax rescale needs no cross-lane traffic.
 // Everything after the K/V rebuild is shared by the two kernels, so the compressed and
 // uncompressed results are identical bit for bit.
 #include <hip/hip_ext.h>

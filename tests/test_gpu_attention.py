@@ -51,7 +51,10 @@ def _ref_case(B, T, Hq, Hkv, seed):
     return q, k, v
 
 
-SHAPES = [(1, 4096, 28, 4), (3, 1000, 32, 8), (2, 333, 32, 32), (4, 17, 16, 2), (2, 500, 64, 2), (1, 1, 8, 1)]
+# KV heads per workgroup gcd(Hkv, 8) = 4, 8, 8, 2, 2, 1, 1, 2: every page-phase count (1,
+# 2, 4, 8), so each loader wavefront serves wavefronts of one phase or of several
+SHAPES = [(1, 4096, 28, 4), (3, 1000, 32, 8), (2, 333, 32, 32), (4, 17, 16, 2), (2, 500, 64, 2), (1, 1, 8, 1),
+          (2, 700, 8, 1), (2, 777, 12, 6)]
 
 
 @pytest.mark.parametrize("B,T,Hq,Hkv", SHAPES)
@@ -71,9 +74,12 @@ def test_attention_bit_identical_and_accurate(B, T, Hq, Hkv):
     assert np.abs(o_c.double().cpu().numpy() - r64).max() < 2e-2       # the reference test's bound
 
 
-@pytest.mark.parametrize("ns_sl", [(1, None), (None, 16), (None, 32), (None, 64), (None, 96)])   # 16: 63 splits, multi-wavefront merge
-def test_split_plans(ns_sl):
-    B, T, Hq, Hkv = 2, 1000, 32, 8
+@pytest.mark.parametrize("T,ns_sl", [(1000, (1, None)), (1000, (None, 16)), (1000, (None, 32)), (1000, (None, 64)),
+                                     (1000, (None, 96)), (2100, (1, None))])
+def test_split_plans(T, ns_sl):
+    # 16: 63 splits (multi-wavefront merge); T 2100 in one split: 132 pages per wavefront,
+    # past the 64 whose page-table entries a wavefront holds in registers
+    B, Hq, Hkv = 2, 32, 8
     q, k, v = _ref_case(B, T, Hq, Hkv, seed=5)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     kc, vc = _encode(kd), _encode(vd)

@@ -65,6 +65,32 @@ def test_paged_matches_contiguous(Hq, Hkv):
     assert_bf16_tolerance(o_pc, oatt.attention(u16(q), u16(k), u16(v), TS, np.float32, lens=lens))
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (28, 4)])
+def test_paged_long_split(Hq, Hkv):
+    """One split over 2048 tokens: a wavefront's pages past the 64 whose block-table entries
+    it (and its loader) holds in registers come through scalar loads of the table."""
+    B, TS = 2, 2048
+    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=54, raw_row_rate=0.01)
+    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=55, raw_row_rate=0.01)
+    q = synthetic.make_q(B, Hq, seed=56)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    npg = TS // P
+    pool_pages = B * npg + 5
+    perm = torch.randperm(pool_pages, generator=torch.Generator().manual_seed(8))[:B * npg]
+    table = perm.view(B, npg).to(torch.int32)
+    kp, vp = _pool(kd, table, pool_pages), _pool(vd, table, pool_pages)
+    kc, vc = _encode(kd), _encode(vd)
+    kpc, vpc = _encode(kp), _encode(vp)
+    bt = table.to(DEV)
+    _say("paged long split", B, TS, Hq, Hkv)
+    o_ref = kernels.attention_compressed(qd, kc, vc, TS, nsplit=1, split_len=TS)
+    o_pc = kernels.attention_compressed(qd, kpc, vpc, TS, nsplit=1, split_len=TS, block_table=bt)
+    o_pb = kernels.attention_reference(qd, kp, vp, TS, nsplit=1, split_len=TS, block_table=bt)
+    assert same_bits(o_pc, o_ref)
+    assert same_bits(o_pb, o_pc)
+    assert_bf16_tolerance(o_pc, oatt.attention(u16(q), u16(k), u16(v), TS, np.float32))
+
+
 def test_paged_shared_prefix_pages():
     """Two sequences whose first pages are the same pool pages (a shared prefix) and a
     third whose table repeats one page: the result is that of the gathered contents."""

@@ -565,12 +565,13 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
 
 // ---- pieces shared by the two split kernels
 
-// Phase merge through LDS: rows of 128 channels padded to kMoRow floats, so that the 16
-// heads of one write land in different banks (a 512-byte row stride put them all in the
-// same ones); both rings hold it.
+// Page-phase partials through LDS (split_epilogue): rows of 128 channels padded to kMoRow
+// floats, so that the 16 heads of one write land in different banks (a 512-byte row
+// stride put them all in the same ones).
 constexpr int kMoRow = kD + 4;
-constexpr int kMoBytes = (kWaves * 16 * kMoRow + 2 * kWaves * 16) * 4;
-static_assert(Ring<true>::bytes >= kMoBytes && Ring<false>::bytes >= kMoBytes, "phase merge must fit the ring");
+constexpr int kMoBytes = (16 * kMoRow + 2 * 16) * 4;    // one wavefront's partial
+static_assert(Ring<true>::per_wave >= kMoBytes && Ring<false>::per_wave >= kMoBytes,
+              "a page phase's partial must fit its wavefront's ring");
 
 // Workgroup coordinates of a split-kernel launch: sequence b, token split, block hb of HW
 // KV heads, group hg of 16 query heads (gh of them real); the split's tokens [start, end)
@@ -711,90 +712,105 @@ __device__ inline void balance_priority(int j, int other) {
     }
 }
 
-// After the page loop: the page phases of each head merged through LDS (same algebra as the
-// split merge) into one partial per (split, query head), then the fused merge when asked
-// for. Every wavefront of the workgroup calls it (its barriers count them all); those with
-// active == false (loader wavefronts) contribute no partial. lds: the workgroup's ring
-// (at least kMoBytes), free by now.
-__device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoords& c, uint8_t* lds, int wave,
-                                               int lane, bool active, int hk, const f32x4 (&acc)[8], float m_i,
-                                               float l_i) {
+// Flags between the wavefronts of a workgroup: LDS words, read and written as relaxed
+// atomics (the waits order the data accesses around them); every wait on one is bounded.
+constexpr int kSpinMax = 1 << 22;                  // bound of every flag wait (a correct run never reaches it)
+__device__ inline int lds_flag_ld(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ inline void lds_flag_st(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+
+// Store one partial row (m, l, o) of a (split, query head): lane (head r, channel group g)
+// holds o for channels 16 nb + 4 g .. + 3; plain stores, or device-scope ones when the
+// split kernel merges in its tail.
+__device__ inline void store_partial(const AttnArgs& a, int64_t prow, int g, const f32x4 (&o)[8], float m, float l) {
+    if (a.counters == nullptr) {
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) *reinterpret_cast<f32x4*>(a.part_o + prow * kD + 16 * nb + 4 * g) = o[nb];
+        if (g == 0) {
+            a.part_m[prow] = m;
+            a.part_l[prow] = l;
+        }
+    } else {
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) st_dev4(a.part_o + prow * kD + 16 * nb + 4 * g, o[nb]);
+        if (g == 0) {
+            st_dev(a.part_m + prow, m);
+            st_dev(a.part_l + prow, l);
+        }
+    }
+}
+
+// After the page loop: one partial per (split, query head). With page phases (fewer than 8
+// KV heads per workgroup), the wavefront of phase p > 0 leaves its (o, m, l) in its own
+// ring -- free once its pages are consumed: o as [16 heads][kMoRow] floats (rows padded so
+// that the 16 heads of one write fall in different banks), then m[16], l[16] -- and raises
+// done[wave]; the phase-0 wavefront of the head slot waits for its partners (bounded),
+// merges in phase order with the split merge's algebra (M = max m, o = sum o 2^(m - M),
+// l likewise) and writes the partial. Then the fused merge when asked for: every
+// wavefront of the workgroup calls this (merge_tail's barriers count them all); active ==
+// false (loader wavefronts) contributes nothing. ring0: the workgroup's first ring (LDS
+// address), ring_stride: bytes from one wavefront's ring to the next.
+__device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoords& c, uint32_t ring0,
+                                               uint32_t ring_stride, int* done, int wave, int lane, bool active,
+                                               int hk, const f32x4 (&acc)[8], float m_i, float l_i) {
     const int r = lane & 15, g = lane >> 4;
     // the accumulators were last written by MFMAs, possibly across inline assembly that the
     // hazard tracking may count as wait states: pad explicitly before the first reads
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     const float l_t = group_sum(l_i);
-    if (c.nphase == 1) {                               // one wavefront per head: write its partial
-        if (active && r < c.gh) {
-            const int64_t prow = ((int64_t)c.b * a.Hq + (int64_t)hk * a.G + c.hg * 16 + r) * a.nsplit + c.split;
-            if (a.counters == nullptr) {
-#pragma unroll
-                for (int nb = 0; nb < 8; ++nb)
-                    *reinterpret_cast<f32x4*>(a.part_o + prow * kD + 16 * nb + 4 * g) = acc[nb];
-                if (g == 0) {
-                    a.part_m[prow] = m_i;
-                    a.part_l[prow] = l_t;
-                }
-            } else {                                   // merged in this kernel: device-scope stores
-#pragma unroll
-                for (int nb = 0; nb < 8; ++nb) st_dev4(a.part_o + prow * kD + 16 * nb + 4 * g, acc[nb]);
-                if (g == 0) {
-                    st_dev(a.part_m + prow, m_i);
-                    st_dev(a.part_l + prow, l_t);
-                }
-            }
-        }
-        merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
-        return;
-    }
-    __syncthreads();
-    float* mo = reinterpret_cast<float*>(lds);            // [wave][16 heads][kMoRow]
-    float* mm = mo + kWaves * 16 * kMoRow;                 // [wave][16]
-    float* ml = mm + kWaves * 16;
-    if (active) {
+    const int phase = wave >> c.hw_sh;
+    auto mo = [&](int w) { return ring0 + (uint32_t)w * ring_stride; };   // wavefront w's partial
+    auto ld_ml = [&](int w, int k) {                                     // k = 0: m, 1: l of head r
+        return *reinterpret_cast<const EXKV_LDS float*>(lds_ptr(mo(w) + 4u * (16 * kMoRow + 16 * k + r)));
+    };
+    if (active && phase > 0) {                         // hand the partial to the phase-0 wavefront
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb)
-            *reinterpret_cast<f32x4*>(mo + (wave * 16 + r) * kMoRow + 16 * nb + 4 * g) = acc[nb];
+            *reinterpret_cast<EXKV_LDS f32x4*>(lds_ptr(mo(wave) + 4u * (r * kMoRow + 16 * nb + 4 * g))) = acc[nb];
         if (g == 0) {
-            mm[wave * 16 + r] = m_i;
-            ml[wave * 16 + r] = l_t;
+            *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave) + 4u * (16 * kMoRow + r))) = m_i;
+            *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave) + 4u * (16 * kMoRow + 16 + r))) = l_t;
         }
-    }
-    __syncthreads();
-    // thread t merges (head slot, head, 4-channel group) items, four channels with the same
-    // per-channel arithmetic as one; waves of one head slot s are s, s + HW, ...
-    for (int idx = threadIdx.x; idx < a.HW * c.gh * (kD / 4); idx += blockDim.x) {
-        const int d = 4 * (idx & (kD / 4 - 1));
-        const int h = (idx >> 5) % c.gh;
-        const int hs = (idx >> 5) / c.gh;
-        float M = -INFINITY;
-        for (int ph = 0; ph < c.nphase; ++ph) M = fmaxf(M, mm[(ph * a.HW + hs) * 16 + h]);
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        float l = 0.f;
-        if (M != -INFINITY) {
-            for (int ph = 0; ph < c.nphase; ++ph) {
-                const int w = ph * a.HW + hs;
-                const float wt = fast_exp2(mm[w * 16 + h] - M);
-                const f32x4 v = *reinterpret_cast<const f32x4*>(mo + (w * 16 + h) * kMoRow + d);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) o[k] += wt * v[k];
-                l += wt * ml[w * 16 + h];
-            }
-        }
-        const int64_t prow =
-            ((int64_t)c.b * a.Hq + (int64_t)(c.hb * a.HW + hs) * a.G + c.hg * 16 + h) * a.nsplit + c.split;
-        if (a.counters == nullptr) {
-            *reinterpret_cast<f32x4*>(a.part_o + prow * kD + d) = o;
-            if (d == 0) {
-                a.part_m[prow] = M;
-                a.part_l[prow] = l;
-            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_flag_st(&done[wave], 1);
+    } else if (active && r < c.gh) {
+        const int64_t prow = ((int64_t)c.b * a.Hq + (int64_t)hk * a.G + c.hg * 16 + r) * a.nsplit + c.split;
+        if (c.nphase == 1) {                           // one wavefront per head: its own partial
+            store_partial(a, prow, g, acc, m_i, l_t);
         } else {
-            st_dev4(a.part_o + prow * kD + d, o);
-            if (d == 0) {
-                st_dev(a.part_m + prow, M);
-                st_dev(a.part_l + prow, l);
+            float M = fmaxf(-INFINITY, m_i);
+            for (int ph = 1; ph < c.nphase; ++ph) {
+                const int w = ph * a.HW + wave;
+                for (int s = 0; s < kSpinMax && lds_flag_ld(&done[w]) == 0; ++s) __builtin_amdgcn_s_sleep(1);
+                asm volatile("" ::: "memory");
+                M = fmaxf(M, ld_ml(w, 0));
             }
+            f32x4 o[8];
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            float l = 0.f;
+            if (M != -INFINITY) {
+                const float wt = fast_exp2(m_i - M);
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) o[nb][k] += wt * acc[nb][k];
+                l += wt * l_t;
+                for (int ph = 1; ph < c.nphase; ++ph) {
+                    const int w = ph * a.HW + wave;
+                    const float wp = fast_exp2(ld_ml(w, 0) - M);
+#pragma unroll
+                    for (int nb = 0; nb < 8; ++nb) {
+                        const f32x4 v = *reinterpret_cast<const EXKV_LDS f32x4*>(
+                            lds_ptr(mo(w) + 4u * (r * kMoRow + 16 * nb + 4 * g)));
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) o[nb][k] += wp * v[k];
+                    }
+                    l += wp * ld_ml(w, 1);
+                }
+            }
+            store_partial(a, prow, g, o, M, l);
         }
     }
     merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
@@ -820,13 +836,8 @@ constexpr int kWpl = kWaves / kLoaders;          // compute wavefronts per loade
 constexpr int kCompThreads = 64 * (kWaves + kLoaders);
 constexpr int kLoadAhead = 3;                    // pages a loader keeps in flight besides the newest
 constexpr int kBytesLoads = kDmaPerPage[1] - 1;  // byte loads per compressed page
-constexpr int kSpinMax = 1 << 22;                // bound of every flag wait (a correct run never reaches it)
 static_assert((kLoadAhead + 1) * kBytesLoads <= 63, "a loader's loads in flight must fit vmcnt");
 
-__device__ inline int lds_flag_ld(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ inline void lds_flag_st(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 
 // Loader wavefront l (see above)
 __device__ __forceinline__ void comp_loader(const AttnArgs& a, const SplitCoords& c, uint32_t lds0, int* ready,
@@ -891,6 +902,7 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
     __shared__ int progress[kWaves];                   // pages done per compute wavefront (priority hint)
     __shared__ int ready[kWaves];                      // pages of wavefront w in its ring (loader -> w)
     __shared__ int avail[kWaves];                      // pages of w its loader may issue (w -> loader)
+    __shared__ int done[kWaves];                       // page phase p > 0: partial left in the ring
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // uniform: scalar addressing
     const SplitCoords c = split_coords(a);
@@ -898,6 +910,7 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
     if (threadIdx.x < kWaves) {
         ready[threadIdx.x] = 0;
         avail[threadIdx.x] = NST - 1;                  // the last stage holds q and the page table at first
+        done[threadIdx.x] = 0;
     }
     __syncthreads();
 
@@ -1041,7 +1054,7 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
             page_softmax_pv(sa, vt, ragged, t0, c.end, c.wlo, g, a.qk_scale, m_i, l_i, acc);
         }
     }
-    split_epilogue(a, c, lds, wave, lane, wave < kWaves, hk, acc, m_i, l_i);
+    split_epilogue(a, c, lds_addr(lds), Ring<true>::per_wave, done, wave, lane, wave < kWaves, hk, acc, m_i, l_i);
 }
 
 // ---- bf16 twin: 8 wavefronts, each issuing its own pages' loads into a 2-stage ring (one
@@ -1051,9 +1064,12 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel<false>(AttnArgs a)
     constexpr int NST = Ring<false>::nst, STB = Ring<false>::stage;
     __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<false>::bytes];
     __shared__ int progress[kWaves];
+    __shared__ int done[kWaves];                       // page phase p > 0: partial left in the ring
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const SplitCoords c = split_coords(a);
+    if (threadIdx.x < kWaves) done[threadIdx.x] = 0;
+    __syncthreads();
     const int hk = c.hb * a.HW + (wave & (a.HW - 1));
     const int phase = wave >> c.hw_sh;
     const int npw = c.npw(phase);
@@ -1138,7 +1154,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel<false>(AttnArgs a)
         read_vt(sb, lo, Ring<false>::vtile, vt);
         page_softmax_pv(sa, vt, ragged, t0, c.end, c.wlo, g, a.qk_scale, m_i, l_i, acc);
     }
-    split_epilogue(a, c, lds, wave, lane, true, hk, acc, m_i, l_i);
+    split_epilogue(a, c, lds_addr(lds), Ring<false>::per_wave, done, wave, lane, true, hk, acc, m_i, l_i);
 }
 
 // Separate merge of up to 32 splits: one wavefront per (sequence, query head) row, every

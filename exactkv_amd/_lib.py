@@ -9,16 +9,16 @@ import os
 
 # EXACTKV_LIB overrides the path of the library to load (default: the in-tree build)
 _PATH = os.environ.get("EXACTKV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 
 # name -> argument types (every entry point returns int: 0 ok, 1 bad argument, 2 HIP error)
 SIGNATURES = {
     "exkv_encode_pages": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
-                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p],
+                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p],
     "exkv_encode_pages_paged": [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64,
-                                _i32, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p],
+                                _i32, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p],
     "exkv_cache_append": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                           _i32, _p],
     "exkv_bf16_append": [_p, _i64, _i64, _p, _p, _i32, _i32, _i32, _i32, _p],

@@ -24,7 +24,7 @@ int hip_status(hipError_t e, const char* where) {
 
 }  // namespace exkv
 
-extern "C" int exkv_abi_version(void) { return 1; }
+extern "C" int exkv_abi_version(void) { return 2; }
 
 extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 

@@ -1,7 +1,8 @@
 // Page encoder, deterministic raw-slot assignment, device-side append and the
 // compressed -> bf16 decoder, for gfx950.
 //
-// Encoding one call's pages takes four launches on the caller's stream:
+// Encoding one call's pages takes four launches on the caller's stream (two when the caller
+// gives a scan workspace: 2-4 then run as one chained scan kernel, scan_chain_kernel):
 //   1. enc_pages_kernel    one wavefront per (sequence, page, head): exponent window,
 //                          zero flag, codes, sign|mantissa bytes, base bytes, rowmask
 //                          (reference kernels.py:216-264, codec.py:31-49);
@@ -340,6 +341,129 @@ static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
     hipLaunchKernelGGL(k, dim3(nb), dim3(1024), 0, stream, a, (int)n);
 }
 
+// ---- two-launch encode: the page kernel, then one scan kernel whose blocks chain
+//
+// scan_chain_kernel: block = kScanUnits units, as scan_write_kernel, but the blocks take
+// their places in ticket order (an atomic counter, so that every block's predecessors have
+// started) and chain their raw-row totals with a decoupled look-back (Merrill & Garland,
+// "Single-pass Parallel Prefix Scan with Decoupled Look-back", NVIDIA technical report
+// NVR-2016-002): a block publishes its total, walks back over its predecessors' published
+// words until one that already includes everything before it, and publishes its inclusive
+// total. Block 0 starts from the pool counter; the last block writes the counter back.
+// rowoff, raw slots and counter come out exactly as from the three-launch scan.
+//
+// Workspace (the caller's; all zero when first used, then only this kernel writes it):
+// ws[0] the ticket counter, ws[1] a call generation, ws[2 + t] block t's word: the call's
+// tag (bits 63-32: the generation's low 31 bits with bit 63 set, so that neither words
+// left by earlier calls nor never-written zero words are taken for this call's), inclusive
+// flag (bit 31), count (bits 30-0). The last ticket holder resets the counter and advances
+// the generation, so consecutive calls on one stream share a workspace; calls that
+// overlap on one workspace race.
+constexpr uint64_t kInclusive = 1ull << 31;
+constexpr int kLookbackSpin = 1 << 22;              // bound of the look-back's waits (never reached)
+
+__device__ inline uint64_t ws_ld(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline void ws_st(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline uint32_t chain_tag(uint32_t gen) { return (gen & 0x7FFFFFFFu) | 0x80000000u; }
+
+// Exclusive prefix of block `t0 + 1` (t0 >= 0): one wavefront reads 64 predecessors' words
+// at a time (lane i: block t - i), nearest first; every word up to the nearest inclusive one
+// must carry this call's tag (else the window is read again), and their counts are summed.
+__device__ inline int64_t chain_lookback(const uint64_t* ws, uint32_t tag, int t0, int lane) {
+    int64_t excl = 0;
+    int t = t0;
+    for (int s = 0; s < kLookbackSpin; ++s) {
+        const int tt = t - lane;
+        const uint64_t st = tt >= 0 ? ws_ld(ws + 2 + tt) : (((uint64_t)tag << 32) | kInclusive);
+        const bool valid = (uint32_t)(st >> 32) == tag;
+        const uint64_t incl = __ballot(valid && (st & kInclusive) != 0);
+        const int stop = incl != 0 ? __builtin_ctzll(incl) : 63;
+        const uint64_t need = stop == 63 ? ~0ull : (2ull << stop) - 1ull;
+        if ((~__ballot(valid) & need) != 0) {          // a predecessor has not published yet
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        // block totals (<= 16 * kScanUnits each) summed in 32 bits, the inclusive word apart
+        int v = lane < stop || (incl == 0 && lane == stop) ? (int)(st & 0x7FFFFFFFull) : 0;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+        excl += v;
+        if (incl != 0)
+            return excl + (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(st & 0x7FFFFFFFull), stop);
+        t -= 64;
+    }
+    return excl;
+}
+
+template <bool PAGED, bool VEC16>
+__global__ void __launch_bounds__(1024) scan_chain_kernel(EncArgs a, int nunits, int nblocks, uint64_t* ws) {
+    __shared__ int s_tile, s_excl;
+    __shared__ uint32_t s_gen;
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x == 0) {
+        const uint32_t gen = (uint32_t)ws_ld(ws + 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the generation is read before the ticket is taken
+        const uint32_t t = __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(ws), 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        if (t == (uint32_t)nblocks - 1u) {             // every ticket of this call is out
+            ws_st(ws, 0ull);
+            ws_st(ws + 1, (uint64_t)(gen + 1u));
+        }
+        s_tile = (int)t;
+        s_gen = gen;
+    }
+    __syncthreads();
+    const int tile = s_tile;
+    const uint32_t tag = chain_tag(s_gen);
+    if ((uint32_t)tile >= (uint32_t)nblocks) return;   // a workspace left inconsistent (misuse): write nothing
+    const int u = tile * kScanUnits + threadIdx.x;
+    int bi = 0, pg = 0, hk = 0;
+    int64_t page = 0;
+    uint32_t m = 0;
+    if (u < nunits) {
+        page = unit_page32<PAGED>(a, u, bi, pg, hk);
+        m = (uint32_t)a.rowmask[page];
+    }
+    int total;
+    const int pre = block_excl_scan(popc32(m), total);   // synchronises
+    if (threadIdx.x < 64) {
+        int64_t excl;
+        if (tile == 0) {
+            excl = *a.cnt;
+            if (lane == 0 && a.before != nullptr) *a.before = (int32_t)excl;
+        } else {
+            if (lane == 0) ws_st(ws + 2 + tile, ((uint64_t)tag << 32) | (uint32_t)total);
+            excl = chain_lookback(ws, tag, tile - 1, lane);
+        }
+        if (lane == 0) {
+            ws_st(ws + 2 + tile, ((uint64_t)tag << 32) | kInclusive | (uint64_t)(uint32_t)(excl + total));
+            if (tile == nblocks - 1) *a.cnt = (int32_t)(excl + total);
+            s_excl = (int)excl;
+        }
+    }
+    __syncthreads();
+    const int off = s_excl + pre;
+    if (u < nunits) a.rowoff[page] = off;
+    copy_escaped_rows<VEC16>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, lane);
+}
+
+// Encode n units: the page kernel, then the chained scan when the workspace has at least
+// 2 + ceil(n / kScanUnits) words, else the three-launch scan.
+static void launch_encode(const EncArgs& a, int64_t n, uint64_t* ws, int64_t ws_words, hipStream_t stream) {
+    hipLaunchKernelGGL(enc_pages_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a, (int)n);
+    const int64_t nb = (n + kScanUnits - 1) / kScanUnits;
+    if (ws == nullptr || ws_words < 2 + nb) {
+        launch_scan(a, n, stream);
+        return;
+    }
+    const bool paged = a.dst_pages != nullptr;
+    const bool vec16 = (uintptr_t)a.src % 16 == 0 && a.s_b % 8 == 0 && a.s_pg % 8 == 0 && a.s_p % 8 == 0 &&
+                       a.s_h % 8 == 0;
+    auto k = paged ? (vec16 ? scan_chain_kernel<true, true> : scan_chain_kernel<true, false>)
+                   : (vec16 ? scan_chain_kernel<false, true> : scan_chain_kernel<false, false>);
+    hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(kScanUnits), 0, stream, a, (int)n, (int)nb, ws);
+}
+
 // Copy one page's raw rows (token p's row at src + p*s_p) into slots rowoff + k (< cap).
 __device__ inline void copy_raw_rows(const uint16_t* src, int64_t s_p, uint32_t m, int32_t off, int64_t cap,
                                      uint16_t* raw, int lane) {
@@ -669,7 +793,7 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
                                  void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
                                  int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
                                  int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
-                                 int32_t D, hipStream_t stream) {
+                                 int32_t D, void* scan_ws, int64_t scan_ws_words, hipStream_t stream) {
     EXKV_REQUIRE(D == kD, "encode_pages: head dim must be 128 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages: TS must be a positive multiple of 16 (got %d)", TS);
     EXKV_REQUIRE(H > 0 && B > 0, "encode_pages: bad H=%d or B=%d", H, B);
@@ -686,11 +810,10 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
     if (n == 0) return EXKV_OK;
     EXKV_REQUIRE(n <= INT32_MAX - 1024, "encode_pages: %lld pages x heads in one call (limit 2^31 - 1025)",
                  (long long)n);
+    EXKV_REQUIRE(scan_ws == nullptr || (uintptr_t)scan_ws % 8 == 0, "encode_pages: scan workspace must be 8-byte aligned");
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
-    const unsigned grid = (unsigned)((n + 3) / 4);
-    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, (int)n);
-    launch_scan(a, n, stream);
+    launch_encode(a, n, (uint64_t*)scan_ws, scan_ws_words, stream);
     return launch_status("encode_pages");
 }
 
@@ -702,7 +825,8 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
                                        void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff,
                                        void* raw, int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows,
                                        int32_t B, const int32_t* dst_pages, int64_t dst_stride, int32_t nb,
-                                       int32_t npg, int32_t H, int32_t TS, int32_t D, hipStream_t stream) {
+                                       int32_t npg, int32_t H, int32_t TS, int32_t D, void* scan_ws,
+                                       int64_t scan_ws_words, hipStream_t stream) {
     EXKV_REQUIRE(D == kD, "encode_pages_paged: head dim must be 128 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages_paged: TS must be a positive multiple of 16 (got %d)", TS);
     EXKV_REQUIRE(H > 0 && B > 0, "encode_pages_paged: bad H=%d or B=%d", H, B);
@@ -722,9 +846,9 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     a.dst_pages = dst_pages;
     a.dst_stride = dst_stride;
     a.all_pages = (int64_t)B * (TS / kPage);
-    const unsigned grid = (unsigned)((n + 3) / 4);
-    hipLaunchKernelGGL(enc_pages_kernel, dim3(grid), dim3(256), 0, stream, a, (int)n);
-    launch_scan(a, n, stream);
+    EXKV_REQUIRE(scan_ws == nullptr || (uintptr_t)scan_ws % 8 == 0,
+                 "encode_pages_paged: scan workspace must be 8-byte aligned");
+    launch_encode(a, n, (uint64_t*)scan_ws, scan_ws_words, stream);
     return launch_status("encode_pages_paged");
 }
 

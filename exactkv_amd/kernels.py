@@ -291,26 +291,45 @@ def _check_source(src, strides, nb, npg, H):
         raise ValueError(f"encode source too small: needs element {last}, has {avail}")
 
 
-def encode_pages(src, strides, buf, b0, pg0, nb, npg):
+_SCAN = {}  # page-encoder scan workspaces per (device, stream)
+
+
+def _scan_ws(dev, units):
+    """The page encoder's chained-scan workspace for the current stream of `dev`: 2 +
+    ceil(units / 1024) int64 words, zero when created (a larger zeroed tensor replaces it
+    when a call needs more). Encodes on one stream run in order, so they share it."""
+    need = 2 + (units + 1023) // 1024
+    key = (dev.index, _lib.stream(dev.index))
+    ws = _SCAN.get(key)
+    if ws is None or ws.numel() < need:
+        ws = _SCAN[key] = torch.zeros(max(need, 1024), dtype=torch.int64, device=dev)
+    return ws
+
+
+def encode_pages(src, strides, buf, b0, pg0, nb, npg, *, chained=True):
     """Page encoder (reference kernels.py:216-268, same arguments). Source page pg0 + p of
     sequence b0 + i sits at src + i*s_b + p*s_pg, its token rows s_p apart and heads s_h
     apart, with (s_b, s_pg, s_p, s_h) = strides in elements; it is written to page pg0 + p
     of cache sequence b0 + i. buf is a cache's encoder view (CompressedKV._buf()): the six
     arrays, the raw-row counter cnt, cap, TS, H, D and optionally 'before', which receives
     the counter's value before the call. Escaped rows take pool slots from the counter on,
-    in (sequence, page, head, token) order."""
+    in (sequence, page, head, token) order. Two launches: the page kernel, then one chained
+    slot scan (in a per-stream workspace); chained=False: the page kernel, then a
+    three-launch scan (same bytes)."""
     H, TS, D = buf["H"], buf["TS"], buf["D"]
     _check_source(src, strides, nb, npg, H)
     raw = buf["raw"]
     before = buf.get("before")
+    ws = _scan_ws(raw.device, int(nb) * int(npg) * H) if chained else None
     _lib.call("exkv_encode_pages", _lib.ptr(src, align=2, what="src"), *[int(s) for s in strides],
               _lib.ptr(buf["sm"]), _lib.ptr(buf["code"]), _lib.ptr(buf["base"]), _lib.ptr(buf["rowmask"]),
               _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4),
               _lib.ptr(before, align=4) if before is not None else None, int(buf["cap"]), raw.shape[0],
-              buf["sm"].shape[0], int(b0), int(pg0), int(nb), int(npg), H, TS, D, _lib.stream())
+              buf["sm"].shape[0], int(b0), int(pg0), int(nb), int(npg), H, TS, D, _lib.ptr(ws),
+              ws.numel() if ws is not None else 0, _lib.stream())
 
 
-def encode_pages_paged(src, strides, buf, dst_pages, nb, npg):
+def encode_pages_paged(src, strides, buf, dst_pages, nb, npg, *, chained=True):
     """encode_pages into a paged cache: page pg of source sequence bi (strides as in
     encode_pages) goes to page dst_pages[bi, pg] of the cache's arrays read as a list of
     B * TS / 16 pages. dst_pages: int32 [>= nb, >= npg] on the GPU."""
@@ -321,12 +340,13 @@ def encode_pages_paged(src, strides, buf, dst_pages, nb, npg):
         raise ValueError("dst_pages must be an int32 [nb, npg] tensor with unit column stride")
     raw = buf["raw"]
     before = buf.get("before")
+    ws = _scan_ws(raw.device, int(nb) * int(npg) * H) if chained else None
     _lib.call("exkv_encode_pages_paged", _lib.ptr(src, align=2, what="src"), *[int(s) for s in strides],
               _lib.ptr(buf["sm"]), _lib.ptr(buf["code"]), _lib.ptr(buf["base"]), _lib.ptr(buf["rowmask"]),
               _lib.ptr(buf["rowoff"]), _lib.ptr(raw), _lib.ptr(buf["cnt"], align=4),
               _lib.ptr(before, align=4) if before is not None else None, int(buf["cap"]), raw.shape[0],
               buf["sm"].shape[0], _lib.ptr(dst_pages, align=4, what="dst_pages"), dst_pages.stride(0), int(nb), int(npg), H,
-              TS, D, _lib.stream())
+              TS, D, _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream())
 
 
 def _paged_append_args(x, table, slots):

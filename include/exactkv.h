@@ -30,7 +30,7 @@ extern "C" {
 
 typedef struct ihipStream_t* hipStream_t;
 
-/* ABI version of the library (1). */
+/* ABI version of the library (2: the encoders take a scan workspace). */
 int exkv_abi_version(void);
 
 /* Message of the last failed call on this thread. */
@@ -42,24 +42,30 @@ const char* exkv_last_error(void);
  * *cnt + running count in (sequence, page, head, token) order; rows whose slot is >= cap
  * are not written, and *cnt advances by the call's total (overflow = *cnt > cap).
  * *before (may be NULL) receives the counter's value before the call.
+ * scan_ws (8-byte aligned, may be NULL): a workspace of scan_ws_words 64-bit words, all zero
+ * when first used and reserved for this library's encodes on one stream; with at least
+ * 2 + ceil(nb*npg*H / 1024) words the encode is two launches (the page kernel, then one
+ * chained slot scan), else four (the page kernel, then a three-launch scan). Same bytes
+ * either way.
  * Replaces: kernels.py:340-346 encode_pages (launch of _encode_pages_kernel :233-268),
  * byte-identical to codec.py:31-55 encode_reference. */
 int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
                       void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
                       int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
                       int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
-                      int32_t D, hipStream_t stream);
+                      int32_t D, void* scan_ws, int64_t scan_ws_words, hipStream_t stream);
 
 /* The page encoder into a paged cache: page pg of source sequence bi goes to page
  * dst_pages[bi*dst_stride + pg] of the B x TS arrays read as a list of B*TS/16 pages (entries
- * clamped to it). Same bytes and raw-slot order as exkv_encode_pages.
+ * clamped to it). Same bytes and raw-slot order as exkv_encode_pages, and the same scan
+ * workspace.
  * No counterpart in the reference (contiguous caches only); paged KV is in its future
  * work (README.md:121-123). */
 int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
                             void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
                             int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
                             const int32_t* dst_pages, int64_t dst_stride, int32_t nb, int32_t npg, int32_t H,
-                            int32_t TS, int32_t D, hipStream_t stream);
+                            int32_t TS, int32_t D, void* scan_ws, int64_t scan_ws_words, hipStream_t stream);
 
 /* Append one token per sequence (x: [B, H, 128] bf16, row strides sx_b, sx_h) to the cache
  * whose token count is state[0] (device): write it into the tail area; when it completes

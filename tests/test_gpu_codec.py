@@ -147,18 +147,19 @@ def _popc16(t):
     return sum((t >> i) & 1 for i in range(16))
 
 
+@pytest.mark.parametrize("chained", [True, False])
 @pytest.mark.parametrize("B,T,H", [(8, 8192, 16), (5, 8192, 32)])
-def test_encoder_slot_scan_full_size(B, T, H):
-    """65,536 units (the one-workgroup scan at its limit) and 81,920 units (the three-launch
-    scan), 5% outlier rows, counter starting at 7: every rowoff is 7 + the raw rows of the
-    units before it in (sequence, page, head) order, the counter ends at 7 + all of them,
-    and decoding gives back every bit."""
+def test_encoder_slot_scan_full_size(B, T, H, chained):
+    """65,536 and 81,920 units, 5% outlier rows, counter starting at 7, through the
+    chained scan (look-back over 64 and 80 blocks) and the three-launch scan:
+    every rowoff is 7 + the raw rows of the units before it in (sequence, page, head)
+    order, the counter ends at 7 + all of them, and decoding gives back every bit."""
     x = synthetic.make_kv(B, T, H, kind="k", seed=31, raw_row_rate=0.05, device=DEV)
-    _say("slot scan", B, T, H, "units", B * (T // 16) * H)
+    _say("slot scan", B, T, H, "units", B * (T // 16) * H, "chained", chained)
     c = exactkv.CompressedKV(B, T, H, 128, reserve=0.08)
     c.cnt.fill_(7)
     st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
-    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16)
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16, chained=chained)
     per = _popc16(c.rowmask).flatten().to(torch.int64)
     n = int(per.sum().item())
     assert n > 0.04 * B * T * H
@@ -166,3 +167,27 @@ def test_encoder_slot_scan_full_size(B, T, H):
     want = 7 + torch.cumsum(per, 0) - per
     assert torch.equal(c.rowoff.flatten().to(torch.int64), want)
     assert same_bits(kernels.decode_to_bf16(c.buffers(), T), x)
+
+
+def test_encoder_chained_equals_multi_launch():
+    """Encodes of different sizes one after another on one stream (the chained scan's
+    workspace is shared: its generation advances between calls), each byte-identical to
+    the three-launch scan on the same input and counter, including
+    a raw pool too small for every raw row (slots past cap skipped, counter past cap)."""
+    cases = [(2, 64, 8, 0.05, 0.5), (4, 4096, 8, 0.02, 0.5), (1, 32, 2, 0.3, 0.5), (3, 1024, 16, 0.05, 0.002),
+             (2, 512, 8, 0.05, 0.5)]
+    for i, (B, T, H, rate, reserve) in enumerate(cases):
+        x = synthetic.make_kv(B, T, H, kind="k", seed=40 + i, raw_row_rate=rate, device=DEV)
+        st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
+        out = []
+        for chained in (True, False):
+            c = exactkv.CompressedKV(B, T, H, 128, reserve=reserve)
+            c.cnt.fill_(3)
+            kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16, chained=chained)
+            out.append(c)
+        a, b = out
+        _say("chained vs three-launch scan", B, T, H, "counter", int(a.cnt.item()), "cap", a.cap)
+        for f in ("sm", "code", "base", "rowmask", "rowoff", "cnt", "_before"):
+            assert torch.equal(getattr(a, f), getattr(b, f)), f
+        n = min(int(a.cnt.item()), a.cap)
+        assert torch.equal(a.raw[:n], b.raw[:n])

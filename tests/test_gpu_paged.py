@@ -128,9 +128,11 @@ def test_paged_bad_arguments_raise():
         kernels.attention_reference(q, k, k, 48, block_table=torch.zeros(1, 2, dtype=torch.int32, device=DEV))
 
 
-def test_paged_encoder_bytes_match_contiguous():
+@pytest.mark.parametrize("chained", [True, False])
+def test_paged_encoder_bytes_match_contiguous(chained):
     """encode_pages_paged writes, at each mapped pool page, the bytes encode_pages writes
-    at the contiguous page (same raw-slot order, so rowoff and raw agree too)."""
+    at the contiguous page (same raw-slot order, so rowoff and raw agree too); through the
+    chained scan and through the three-launch scan."""
     B, TS, H = 3, 512, 8
     npg = TS // P
     x = synthetic.make_kv(B, TS, H, kind="k", seed=71, raw_row_rate=0.02).to(DEV)
@@ -140,7 +142,7 @@ def test_paged_encoder_bytes_match_contiguous():
     pool = exactkv.CompressedKV(1, pool_pages * P, H, 128, reserve=1.0)
     st = (x.stride(0), P * x.stride(1), x.stride(1), x.stride(2))
     _say("paged encode", B, TS, H, pool_pages)
-    kernels.encode_pages_paged(x, st, pool._buf(), table.to(torch.int32).to(DEV), B, npg)
+    kernels.encode_pages_paged(x, st, pool._buf(), table.to(torch.int32).to(DEV), B, npg, chained=chained)
     n = int(c.cnt.item())
     assert n > 0 and int(pool.cnt.item()) == n
     tl = table.reshape(-1).to(DEV)

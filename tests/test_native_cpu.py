@@ -38,13 +38,15 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == 1 and b"head dim" in lib.exkv_last_error()
     rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 5000, 4096, None, 0, 1, 4096, 0, 0.1, None)
     assert rc == 1 and b"outside" in lib.exkv_last_error()
-    rc = lib.exkv_encode_pages(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 1, 0, 2, 1, 4, 64, 128, None)
+    rc = lib.exkv_encode_pages(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 1, 0, 2, 1, 4, 64, 128, None, 0,
+                               None)
     assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
     with pytest.raises(RuntimeError, match="split_len"):
         _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0, 0.1, None)
     # paged entry points: a page table narrower than the pages to encode, a raw pool
     # without room for the tail areas, more rows than sequence slots
-    rc = lib.exkv_encode_pages_paged(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 1, 1, 2, 1, 3, 4, 64, 128, None)
+    rc = lib.exkv_encode_pages_paged(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 1, 1, 2, 1, 3, 4, 64, 128, None,
+                                     0, None)
     assert rc == 1 and b"page table" in lib.exkv_last_error()
     rc = lib.exkv_cache_append_paged(1, 0, 0, 1, 1, 1, 1, 1, 1, 1, 1, 10, 100, None, 1, 1, 8, 2, 4, 2, 8, 16, 128,
                                      None)

@@ -27,7 +27,7 @@ How CompressedKV is organised here:
 import torch
 
 from . import _lib
-from .kernels import encode_pages, P
+from .kernels import encode_pages, HEAD_DIMS, P
 
 _FIELDS = ("sm", "code", "base", "rowmask", "rowoff", "raw")
 
@@ -38,11 +38,12 @@ def _device_words(n, dev):
 
 class CompressedKV:
     def __init__(self, B, TS, H, D, device="cuda", reserve=0.01):
-        """B sequences of up to TS tokens (a multiple of 16), H KV heads of dimension D (128).
-        reserve: escaped-row slots to start with, as a fraction of B*TS*H rows (the pool
-        grows on demand; it never starts below one page step of every sequence and head)."""
-        if TS % P != 0 or D != 128:
-            raise AssertionError(f"the format needs TS % {P} == 0 and head dim 128 (got TS={TS}, D={D})")
+        """B sequences of up to TS tokens (a multiple of 16), H KV heads of dimension D (64,
+        128 or 256; the reference stores 128 only, cache.py:21). reserve: escaped-row slots
+        to start with, as a fraction of B*TS*H rows (the pool grows on demand; it never
+        starts below one page step of every sequence and head)."""
+        if TS % P != 0 or D not in HEAD_DIMS:
+            raise AssertionError(f"the format needs TS % {P} == 0 and head dim in {HEAD_DIMS} (got TS={TS}, D={D})")
         dev = torch.device(device)
         self.B, self.TS, self.H, self.D, self.dev = B, TS, H, D, dev
         npages = TS // P

@@ -21,7 +21,7 @@ CPU implementation in this package.
 """
 import torch
 
-from .kernels import encode_pages, decode_to_bf16, P
+from .kernels import encode_pages, decode_to_bf16, HEAD_DIMS, P
 
 
 def _gpu(dev):
@@ -33,9 +33,12 @@ def _gpu(dev):
 
 
 def encode_reference(x):
-    """x: [B, T, H, D] bf16, T a multiple of 16. Returns a dict of tensors (raw rows in page order)."""
+    """x: [B, T, H, D] bf16, T a multiple of 16, D in HEAD_DIMS. Returns a dict of tensors
+    (raw rows in page order)."""
     B, T, H, D = x.shape
     assert T % P == 0 and x.dtype == torch.bfloat16
+    if D not in HEAD_DIMS:
+        raise ValueError(f"head dim {D}: the GPU codec is built for {HEAD_DIMS}")
     dev = _gpu(x.device)
     xd = x.to(dev).contiguous()
     NP = T // P
@@ -79,8 +82,8 @@ _STORED = ("sm", "code", "base", "rowmask", "rowoff", "raw")
 def bits_per_value(c):
     """Storage cost of an encoded tensor (reference codec.py:76-78): every allocated byte of
     the six arrays, raw pool included, in bits per value of the [B, T, H, D] input. With N
-    raw rows that is 8 * (192 + 128/16 + 8/16 + 256 N / (B T H)) / 128 = 12.53125 +
-    16 N / (B T H) for D = 128."""
+    raw rows that is 8 * (1.5 D + D/16 + 8/16 + 2 D N / (B T H)) / D = 12.5 + 4 / D +
+    16 N / (B T H) (12.53125 + 16 N / (B T H) for D = 128)."""
     values = 1
     for n in c["sm"].shape:
         values *= n

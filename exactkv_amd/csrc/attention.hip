@@ -131,6 +131,7 @@ struct AttnArgs {
     const int32_t* block_table;
     int64_t bt_stride;
     int pool_pages;
+    int D;                    // head dim: 128 (the tuned kernels), 64 or 256 (attn_dgen_kernel)
 };
 
 // ---- split merge (kernels.py:33-43): M = max_s m_s, w_s = 2^(m_s - M),
@@ -660,8 +661,9 @@ __device__ inline void zero_invalid_rows(bool valid, uint32_t (&d)[16]) {
 // max(s) * scale == max(s * scale) (rounding is monotone), and the scale goes into the
 // exponent's fma: p = 2^(s * scale - m). Tokens outside the split or the window score
 // -inf; only a ragged page has any. p is rounded to bf16 for P.V, l sums the fp32 p.
-__device__ __forceinline__ void page_softmax_pv(f32x4 sa, const s16x4 (&vt)[8], bool ragged, int t0, int end, int wlo,
-                                                int g, float qk_scale, float& m_i, float& l_i, f32x4 (&acc)[8]) {
+template <int NB>
+__device__ __forceinline__ void page_softmax_pv(f32x4 sa, const s16x4 (&vt)[NB], bool ragged, int t0, int end, int wlo,
+                                                int g, float qk_scale, float& m_i, float& l_i, f32x4 (&acc)[NB]) {
     // The score MFMAs' result is read below after branches whose opaque asm the compiler's
     // hazard tracking has counted as wait states (reads then saw stale accumulators). Pass
     // it through 16 explicit wait states instead: the asm defines sa, so every later read
@@ -690,13 +692,13 @@ __device__ __forceinline__ void page_softmax_pv(f32x4 sa, const s16x4 (&vt)[8], 
     m_i = m_new;
     if (__ballot(alpha != 1.f) != 0) {                 // rescale only when some head's max moved
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) acc[nb] *= alpha;
+        for (int nb = 0; nb < NB; ++nb) acc[nb] *= alpha;
     }
     // O^T += V^T P^T: V^T rows 4g..4g+3 of channel 16nb + r; the C layout of S^T is exactly
     // the P^T operand layout, and O^T accumulates with lane = head
     const s16x4 pop = __builtin_bit_cast(s16x4, pb4);
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[nb], pop, acc[nb], 0, 0, 0);
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[nb], pop, acc[nb], 0, 0, 0);
 }
 
 // Wavefronts w and w ^ 4 share a SIMD, whose issue arbiter favours the older one: left
@@ -1239,6 +1241,252 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
     }
 }
 
+
+// ---- split kernel for head dims 64 and 256 (the reference builds head dim 128 only,
+// cache.py:21; its kernels.py:142-194 at other head sizes)
+//
+// Grid: x = split, y = (sequence, KV head, group of 16 query heads). NPH wavefronts per
+// workgroup (page phases: 4 for D = 64, 2 for D = 256) take the split's pages round robin
+// and are merged through LDS at the end, one partial per (split, query head), so the
+// workspace and the merge are those of the D = 128 kernels. Per page, each lane (token r,
+// channel group g) loads its share of the K and V bytes straight into VGPRs (the next
+// page's loads in flight behind the current page's work where registers allow), rebuilds
+// the values (tile.hpp, any head dim), splices raw rows from the pool, and runs the score
+// MFMAs, softmax and P.V of the D = 128 kernels: S^T = K Q^T with
+// v_mfma_f32_16x16x32_bf16 over D/32 k-blocks, V through a per-wavefront LDS tile (rows
+// of 2D + 32 bytes, so that the transposed reads touch every bank exactly twice) read as
+// the V^T operand with ds_read_b64_tr_b16 (lane (r, g) supplies row 4g + r/4, channels
+// 16nb + 4(r & 3) .. + 3, and receives channel 16nb + r of rows 4g .. 4g + 3). The bf16
+// twin is the same template over plain rows, so the two agree bit for bit.
+template <int D>
+struct DGen {
+    static constexpr int NPH = D >= 256 ? 2 : 4;     // page phases (wavefronts) per workgroup
+    static constexpr int V = Run<D>::V;             // value dwords per lane (K or V of a page)
+    static constexpr int KC = D / 32;               // score MFMA k-blocks
+    static constexpr int NB = D / 16;               // 16-channel blocks of V and O
+    static constexpr int TROW = 2 * D + 32;         // V tile row (bytes)
+    static constexpr int TILE = kPage * TROW;
+    static constexpr int MROW = D + 4;              // one head's partial in the merge (floats)
+    static constexpr int MBYTES = (16 * MROW + 32) * 4;
+    static constexpr int LDS = NPH * TILE + (NPH - 1) * MBYTES;
+};
+
+// One page as loaded by a lane: the K and V bytes (compressed) or values (bf16 twin).
+template <int D, bool COMP>
+struct DPage;
+template <int D>
+struct DPage<D, true> {
+    PageBytesD<D> k, v;
+    uint32_t mk, mv;
+    int32_t ok, ov;
+};
+template <int D>
+struct DPage<D, false> {
+    uint32_t k[Run<D>::V], v[Run<D>::V];
+};
+
+template <int D, bool COMP>
+__device__ inline void dgen_load(const AttnArgs& a, int b, int NP, int p, int hk, int r, int g, DPage<D, COMP>& pg) {
+    const int64_t pidx = a.block_table == nullptr
+                             ? (int64_t)b * NP + p
+                             : (int64_t)min((uint32_t)a.block_table[b * a.bt_stride + p], (uint32_t)(a.pool_pages - 1));
+    const int64_t row = (pidx * kPage + r) * a.Hkv + hk, page = pidx * a.Hkv + hk;
+    if constexpr (COMP) {
+        load_page_d<D>(a.k, row, page, g, pg.k);
+        load_page_d<D>(a.v, row, page, g, pg.v);
+        pg.mk = (uint32_t)a.k.rowmask[page];
+        pg.mv = (uint32_t)a.v.rowmask[page];
+        pg.ok = a.k.rowoff[page];
+        pg.ov = a.v.rowoff[page];
+    } else {
+        load_row_values_d<D>(a.kb + row * D, g, pg.k);
+        load_row_values_d<D>(a.vb + row * D, g, pg.v);
+    }
+}
+
+template <int D, bool COMP>
+__global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a) {
+    using G = DGen<D>;
+    constexpr int R = Run<D>::R;
+    constexpr bool kPrefetch = !(COMP && D >= 256);   // registers for a second page in flight
+    __shared__ __attribute__((aligned(16))) uint8_t lds[G::LDS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x;
+    int y = blockIdx.y;
+    const int hg = y % a.HG;
+    y /= a.HG;
+    const int hk = y % a.Hkv, b = y / a.Hkv;
+    int len = a.lens ? a.lens[b * a.lens_stride] : a.T;
+    len = min(max(len, 0), a.TS);
+    const int wlo = a.window > 0 ? max(len - a.window, 0) : 0;   // sliding window: tokens [wlo, len)
+    const int start = (wlo & ~(kPage - 1)) + split * a.split_len;
+    const int end = min(start + a.split_len, len);
+    const int NP = a.TS / kPage, p0 = start / kPage, pend = end > start ? (end + kPage - 1) / kPage : p0;
+    const int gh = min(16, a.G - hg * 16);
+
+    // Q^T operand: column = head hg*16 + r, k-block kc = channels of dwords 4kc.. of a lane's values
+    bf16x8 qop[G::KC];
+    {
+        const uint16_t* qr = a.q + ((int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16 + min(r, gh - 1)) * D;
+#pragma unroll
+        for (int kc = 0; kc < G::KC; ++kc) {
+            const int d0 = kc < G::KC / 2 ? g * R + 8 * kc : D / 2 + g * R + 8 * (kc - G::KC / 2);
+            uint4 v = *reinterpret_cast<const uint4*>(qr + d0);
+            if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
+            qop[kc] = as_bf16x8(v.x, v.y, v.z, v.w);
+        }
+    }
+    f32x4 acc[G::NB];
+#pragma unroll
+    for (int nb = 0; nb < G::NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_i = -INFINITY, l_i = 0.f;
+    const uint32_t tile = lds_addr(lds) + (uint32_t)(wave * G::TILE);
+    const uint32_t tw = tile + (uint32_t)(r * G::TROW + 2 * g * R);                     // V tile row r, low run
+    const uint32_t tr = tile + (uint32_t)((4 * g + (r >> 2)) * G::TROW + 8 * (r & 3));  // transpose reads
+
+    DPage<D, COMP> cur, nxt;
+    int p = p0 + wave;
+    if (p < pend) dgen_load<D, COMP>(a, b, NP, p, hk, r, g, cur);
+    for (; p < pend; p += G::NPH) {
+        const int pn = p + G::NPH;
+        if (kPrefetch && pn < pend) dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, nxt);
+        uint32_t kd[G::V], vd[G::V];
+        if constexpr (COMP) {
+            rebuild_values_d<D>(cur.k, kd);
+            if (cur.mk != 0u && ((cur.mk >> r) & 1u))
+                load_row_values_d<D>(a.k.raw + raw_slot(cur.mk, cur.ok, r, a.k.raw_rows) * D, g, kd);
+            rebuild_values_d<D>(cur.v, vd);
+            if (cur.mv != 0u && ((cur.mv >> r) & 1u))
+                load_row_values_d<D>(a.v.raw + raw_slot(cur.mv, cur.ov, r, a.v.raw_rows) * D, g, vd);
+        } else {
+#pragma unroll
+            for (int i = 0; i < G::V; ++i) {
+                kd[i] = cur.k[i];
+                vd[i] = cur.v[i];
+            }
+        }
+        const int t0 = p * kPage;
+        const bool ragged = t0 < wlo || t0 + kPage > end;
+        if (ragged) {                                  // rows outside [wlo, end) read as zero V
+            keep_branch();
+            if (t0 + r < wlo || t0 + r >= end) {
+#pragma unroll
+                for (int i = 0; i < G::V; ++i) vd[i] = 0u;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) {              // the two runs of row r into the V tile
+            lds_st16(lds_ptr(tw) + 16 * i, vd[4 * i], vd[4 * i + 1], vd[4 * i + 2], vd[4 * i + 3]);
+            lds_st16(lds_ptr(tw) + D + 16 * i, vd[R / 2 + 4 * i], vd[R / 2 + 4 * i + 1], vd[R / 2 + 4 * i + 2],
+                     vd[R / 2 + 4 * i + 3]);
+        }
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < G::KC; ++kc)
+            sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]),
+                                                         qop[kc], sa, 0, 0, 0);
+        s16x4 vt[G::NB];
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb)
+            vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
+        page_softmax_pv<G::NB>(sa, vt, ragged, t0, end, wlo, g, a.qk_scale, m_i, l_i, acc);
+        if constexpr (kPrefetch) {
+            cur = nxt;
+        } else if (pn < pend) {
+            dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, cur);
+        }
+    }
+
+    // page phases -> one partial per (split, query head): phase w > 0 leaves (o, m, l) in
+    // the merge area, phase 0 merges them in order (M = max m, o = sum o 2^(m - M), l alike)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    const float l_t = group_sum(l_i);
+    const uint32_t mb = lds_addr(lds) + (uint32_t)(G::NPH * G::TILE);
+    auto mo = [&](int w) { return mb + (uint32_t)((w - 1) * G::MBYTES); };
+    if (wave > 0) {
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb)
+            *reinterpret_cast<EXKV_LDS f32x4*>(lds_ptr(mo(wave) + 4u * (r * G::MROW + 16 * nb + 4 * g))) = acc[nb];
+        if (g == 0) {
+            *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave) + 4u * (16 * G::MROW + r))) = m_i;
+            *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave) + 4u * (16 * G::MROW + 16 + r))) = l_t;
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && r < gh) {
+        auto ld_ml = [&](int w, int k) {
+            return *reinterpret_cast<const EXKV_LDS float*>(lds_ptr(mo(w) + 4u * (16 * G::MROW + 16 * k + r)));
+        };
+        float M = fmaxf(-INFINITY, m_i);
+        for (int w = 1; w < G::NPH; ++w) M = fmaxf(M, ld_ml(w, 0));
+        f32x4 o[G::NB];
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float l = 0.f;
+        if (M != -INFINITY) {
+            const float wt = fast_exp2(m_i - M);
+#pragma unroll
+            for (int nb = 0; nb < G::NB; ++nb)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[nb][k] += wt * acc[nb][k];
+            l += wt * l_t;
+            for (int w = 1; w < G::NPH; ++w) {
+                const float wp = fast_exp2(ld_ml(w, 0) - M);
+#pragma unroll
+                for (int nb = 0; nb < G::NB; ++nb) {
+                    const f32x4 v = *reinterpret_cast<const EXKV_LDS f32x4*>(
+                        lds_ptr(mo(w) + 4u * (r * G::MROW + 16 * nb + 4 * g)));
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) o[nb][k] += wp * v[k];
+                }
+                l += wp * ld_ml(w, 1);
+            }
+        }
+        const int64_t prow = ((int64_t)b * a.Hq + (int64_t)hk * a.G + hg * 16 + r) * a.nsplit + split;
+#pragma unroll
+        for (int nb = 0; nb < G::NB; ++nb) *reinterpret_cast<f32x4*>(a.part_o + prow * D + 16 * nb + 4 * g) = o[nb];
+        if (g == 0) {
+            a.part_m[prow] = M;
+            a.part_l[prow] = l;
+        }
+    }
+}
+
+// Split merge for head dims 64 and 256: one wavefront per (sequence, query head) row, lane
+// = D/64 consecutive channels, the splits summed in order with fmas (out = sum o_s w_s /
+// sum l_s w_s, w_s = 2^(m_s - max m)). Used by the compressed call and its twin alike.
+template <int D>
+__global__ void __launch_bounds__(64) attn_reduce_d_kernel(const float* po, const float* pm, const float* pl,
+                                                           uint16_t* out, int ns) {
+    constexpr int C = D / 64;
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const float* m = pm + row * ns;
+    const float* l = pl + row * ns;
+    const float* o = po + row * ns * D + lane * C;
+    float M = -INFINITY;
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, m[s]);
+    M = wave_max(M);
+    float n[C], den = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) n[c] = 0.f;
+    for (int s = 0; s < ns; ++s) {
+        const float w = fast_exp2(m[s] - M);
+        const float* os = o + (int64_t)s * D;
+#pragma unroll
+        for (int c = 0; c < C; ++c) n[c] = __builtin_fmaf(os[c], w, n[c]);
+        den = __builtin_fmaf(l[s], w, den);
+    }
+    uint16_t* dst = out + row * D + lane * C;
+    if constexpr (C == 1) {
+        const __bf16 v = (__bf16)(n[0] / den);
+        dst[0] = __builtin_bit_cast(uint16_t, v);
+    } else {
+#pragma unroll
+        for (int c = 0; c < C; c += 2) reinterpret_cast<uint32_t*>(dst)[c / 2] = pack_bf16x2(n[c] / den, n[c + 1] / den);
+    }
+}
+
 }  // namespace exkv
 
 using namespace exkv;
@@ -1256,7 +1504,7 @@ static int heads_per_block(int Hkv) {
 
 static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_t* lens, int nsplit,
                       int split_len, int window) {
-    EXKV_REQUIRE(D == kD, "attention: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "attention: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "attention: bad heads Hq=%d Hkv=%d (B=%d)", Hq,
                  Hkv, B);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "attention: TS=%d must be a positive multiple of 16", TS);
@@ -1273,7 +1521,7 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
         EXKV_REQUIRE((int64_t)nsplit * split_len >= min((int64_t)TS, reach),
                      "attention: with per-sequence lengths the splits must cover TS=%d (window %d)", TS, window);
     }
-    EXKV_REQUIRE((int64_t)B * (Hkv / heads_per_block(Hkv)) * ((Hq / Hkv + 15) / 16) < 65536,
+    EXKV_REQUIRE((int64_t)B * (D == kD ? Hkv / heads_per_block(Hkv) : Hkv) * ((Hq / Hkv + 15) / 16) < 65536,
                  "attention: too many (sequence, head block) units");
     return EXKV_OK;
 }
@@ -1282,10 +1530,27 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
 // and end (hipExtLaunchKernelGGL), consumed by that launch.
 static thread_local hipEvent_t t_split_start = nullptr, t_split_stop = nullptr;
 
+template <int D>
+static void launch_dgen(bool comp, const AttnArgs& a, hipEvent_t e0, hipEvent_t e1, hipStream_t stream) {
+    const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * a.Hkv * a.HG)), block(64 * DGen<D>::NPH);
+    auto k = comp ? attn_dgen_kernel<D, true> : attn_dgen_kernel<D, false>;
+    if (e0 || e1)
+        hipExtLaunchKernelGGL(k, grid, block, 0, stream, e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(k, grid, block, 0, stream, a);
+}
+
 static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * (a.Hkv / a.HW) * a.HG));
     hipEvent_t e0 = t_split_start, e1 = t_split_stop;
     t_split_start = t_split_stop = nullptr;
+    if (a.D != kD) {
+        if (a.D == 64)
+            launch_dgen<64>(comp, a, e0, e1, stream);
+        else
+            launch_dgen<256>(comp, a, e0, e1, stream);
+        return hip_status(hipGetLastError(), comp ? "attn_split_compressed" : "attn_split_bf16");
+    }
     if (e0 || e1) {
         if (comp)
             hipExtLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(kCompThreads), 0, stream, e0, e1, 0, a);
@@ -1311,9 +1576,13 @@ extern "C" int exkv_time_next_split(hipEvent_t start, hipEvent_t stop) {
     return EXKV_OK;
 }
 
-static int launch_reduce(const float* o, const float* m, const float* l, void* out, int64_t rows, int ns,
+static int launch_reduce(const float* o, const float* m, const float* l, void* out, int64_t rows, int ns, int D,
                          hipStream_t stream) {
-    if (ns <= 32)
+    if (D == 64)
+        hipLaunchKernelGGL(attn_reduce_d_kernel<64>, dim3((unsigned)rows), dim3(64), 0, stream, o, m, l, (uint16_t*)out, ns);
+    else if (D == 256)
+        hipLaunchKernelGGL(attn_reduce_d_kernel<256>, dim3((unsigned)rows), dim3(64), 0, stream, o, m, l, (uint16_t*)out, ns);
+    else if (ns <= 32)
         hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rows), dim3(64), 0, stream, o, m, l, (uint16_t*)out, ns);
     else
         hipLaunchKernelGGL(attn_reduce_wide_kernel, dim3((unsigned)rows, kD / kWideChunk), dim3(64 * kWideWaves), 0,
@@ -1345,6 +1614,7 @@ static int fill_compressed(AttnArgs& a, const void* q, const void* k_sm, const v
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
     a.HW = heads_per_block(Hkv);
+    a.D = D;
     return EXKV_OK;
 }
 
@@ -1363,6 +1633,7 @@ static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, f
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
     a.HW = heads_per_block(Hkv);
+    a.D = D;
     return EXKV_OK;
 }
 
@@ -1385,13 +1656,13 @@ extern "C" int exkv_attn_compressed(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, E
     int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits) {         // merge fused into the split kernel
+    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {   // merge fused into the split kernel (D = 128)
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(true, a, stream);
     }
     rc = launch_split(true, a, stream);
-    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, D, stream);
 }
 
 extern "C" int exkv_attn_split_compressed(EXKV_C_PARAMS, EXKV_SHAPE_PARAMS, hipStream_t stream) {
@@ -1406,13 +1677,13 @@ extern "C" int exkv_attn_bf16(const void* q, const void* k, const void* v, float
     int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits) {
+    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(false, a, stream);
     }
     rc = launch_split(false, a, stream);
-    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, D, stream);
 }
 
 extern "C" int exkv_attn_split_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m,
@@ -1445,13 +1716,13 @@ extern "C" int exkv_attn_compressed_paged(EXKV_C_PARAMS, int32_t* ws_cnt, void* 
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed_paged: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits) {
+    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(true, a, stream);
     }
     rc = launch_split(true, a, stream);
-    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, D, stream);
 }
 
 extern "C" int exkv_attn_split_compressed_paged(EXKV_C_PARAMS, const int32_t* block_table, int64_t bt_stride,
@@ -1470,19 +1741,19 @@ extern "C" int exkv_attn_bf16_paged(const void* q, const void* k, const void* v,
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16_paged: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits) {
+    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
         a.out = (uint16_t*)out;
         a.counters = ws_cnt;
         return launch_split(false, a, stream);
     }
     rc = launch_split(false, a, stream);
-    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, stream);
+    return rc ? rc : launch_reduce(ws_o, ws_m, ws_l, out, (int64_t)B * Hq, nsplit, D, stream);
 }
 
 extern "C" int exkv_attn_reduce(const float* ws_o, const float* ws_m, const float* ws_l, void* out, int64_t rows,
                                 int32_t nsplit, int32_t D, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "attn_reduce: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "attn_reduce: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(rows > 0 && nsplit > 0, "attn_reduce: bad rows=%lld nsplit=%d", (long long)rows, nsplit);
     EXKV_REQUIRE(ws_o && ws_m && ws_l && out, "attn_reduce: null pointer");
-    return launch_reduce(ws_o, ws_m, ws_l, out, rows, nsplit, stream);
+    return launch_reduce(ws_o, ws_m, ws_l, out, rows, nsplit, D, stream);
 }

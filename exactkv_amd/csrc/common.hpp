@@ -2,7 +2,7 @@
 //
 // Byte format (reference exactkv/codec.py:1-25): per (sequence, 16-token page, KV head,
 // channel) one base byte; per element a sign|mantissa byte and a 4-bit exponent code,
-// where code byte j of a row holds channel j (low nibble) and channel j + 64 (high
+// where code byte j of a row holds channel j (low nibble) and channel j + D/2 (high
 // nibble). base < 128: exponent = base + code. base >= 128 (a group with zeros):
 // code 0 means exponent 0, otherwise exponent = base - 128 + code.
 #pragma once
@@ -13,7 +13,11 @@
 namespace exkv {
 
 constexpr int kPage = 16;     // tokens per page
-constexpr int kD = 128;       // head dimension (the only one the format supports)
+constexpr int kD = 128;       // head dimension of the tuned attention kernels
+
+// Head dimensions the kernels are built for: 128 (Qwen2/2.5/3, Llama-3), 64 (the small
+// Qwen2.5 and Llama-3.2 models) and 256.
+__host__ __device__ constexpr bool head_dim_ok(int D) { return D == 64 || D == 128 || D == 256; }
 
 // ---------------------------------------------------------------- bit helpers
 

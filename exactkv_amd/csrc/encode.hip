@@ -36,90 +36,111 @@ __device__ inline u16x2 vsubs(u16x2 a, u16x2 b) { return __builtin_elementwise_s
 // bytes 0 and 2 of x as a 16-bit value
 __device__ inline uint16_t bytes02(uint32_t x) { return (uint16_t)__builtin_amdgcn_perm(0u, x, 0x0c0c0200u); }
 
-// Encode one 16-token page of one head. Lane l = (half, m): tokens 8*half .. 8*half+7,
-// channels 2m, 2m+1 (word lo) and 2m+64, 2m+65 (word hi) -- so each code byte (channel j
-// low nibble, j + 64 high nibble) and each pair of sm / code bytes is produced by one lane,
-// and every load and store moves two channels. Per channel, with e the 8-bit exponent:
+// Encode one 16-token page of one head of D channels (D = 64, 128, 256). The lanes form
+// NG token groups (2; 4 for D = 64) of CL = 64 / NG lanes: lane (grp, m) takes tokens
+// TPL*grp .. TPL*grp + TPL - 1 (TPL = 16 / NG) and, in pass p, channels c, c + 1 (word lo)
+// and c + D/2, c + D/2 + 1 (word hi) with c = 2 CL p + 2m -- so each code byte (channel j
+// low nibble, j + D/2 high nibble) and each pair of sm / code bytes is produced by one
+// lane, and every load and store moves two channels (one pass for D <= 128, two for 256).
+// Per channel, with e the 8-bit exponent:
 //   top = max e over the 16 tokens, floor = max(top - 15, 0), zf = (some e == 0) && floor > 0,
 //   nibble = max(e - floor, 0) (e <= top keeps it <= 15; e == 0 gives 0 either way),
 //   a row is raw if some channel has e != 0 && e < floor + zf, or if any floor >= 128;
 // the same rule as the reference's per-element test (code >= 1 for a non-zero in a
 // flagged group, code >= 0 otherwise, floor < 128), in packed 16-bit integer arithmetic.
-// The two halves combine their per-channel maxima and minima with one cross-half shuffle
-// each. Token p's source row is src + p * s_p, except row 15 which comes from `last` when
-// given; rows must be 4-byte aligned (even element offsets: callers check). Destination
-// rows of consecutive tokens are `rs` rows apart (rs = H).
+// The token groups combine their per-channel maxima and minima with one cross-group
+// shuffle each (two for four groups). Token p's source row is src + p * s_p, except row
+// 15 which comes from `last` when given; rows must be 4-byte aligned (even element
+// offsets: callers check). Destination rows of consecutive tokens are `rs` rows apart
+// (rs = H).
+template <int D>
 __device__ __attribute__((always_inline)) inline void encode_page(const uint16_t* src, int64_t s_p,
                                                                   const uint16_t* last, int lane,
                                                                   uint8_t* sm0, uint8_t* code0, int64_t rs,
                                                                   uint8_t* basep, int32_t* rmaskp) {
-    const int half = lane >> 5, m = lane & 31;
-    // per-lane row-0 addresses of the lane's half; token i of the half is i strides on
-    const uint16_t* srow = src + (int64_t)(8 * half) * s_p + 2 * m;
-    const int64_t sm_stride = rs * 128, code_stride = rs * 64;
-    uint8_t* smrow = sm0 + (int64_t)(8 * half) * sm_stride + 2 * m;
-    uint8_t* coderow = code0 + (int64_t)(8 * half) * code_stride + 2 * m;
-    uint32_t lo[8], hi[8];                             // bf16 pairs: channels (2m, 2m+1), (2m+64, 2m+65)
+    static_assert(D == 64 || D == 128 || D == 256, "head dim 64, 128 or 256");
+    constexpr int NG = D == 64 ? 4 : 2;            // token groups
+    constexpr int TPL = kPage / NG;                // tokens per lane
+    constexpr int CL = 64 / NG;                    // lanes per group = channel pairs per pass
+    constexpr int HALF = D / 2;
+    constexpr int NPASS = HALF / (2 * CL);
+    const int grp = lane / CL, m = lane % CL;
+    const int64_t sm_stride = rs * D, code_stride = rs * HALF;
+    uint32_t esc = 0;                              // bit i: token TPL*grp + i escapes
+    bool big = false;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint16_t* rp = (i == 7 && half == 1 && last != nullptr) ? last + 2 * m : srow + i * s_p;
-        lo[i] = *reinterpret_cast<const uint32_t*>(rp);
-        hi[i] = *reinterpret_cast<const uint32_t*>(rp + 64);
-    }
-    u16x2 elo[8], ehi[8];                              // exponents, one channel per 16-bit lane
+    for (int pass = 0; pass < NPASS; ++pass) {
+        const int c = 2 * CL * pass + 2 * m;
+        // per-lane row-0 addresses of the lane's group; token i of the group is i strides on
+        const uint16_t* srow = src + (int64_t)(TPL * grp) * s_p + c;
+        uint8_t* smrow = sm0 + (int64_t)(TPL * grp) * sm_stride + c;
+        uint8_t* coderow = code0 + (int64_t)(TPL * grp) * code_stride + c;
+        uint32_t lo[TPL], hi[TPL];                 // bf16 pairs: channels (c, c+1), (c+D/2, c+D/2+1)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        elo[i] = as_u16x2((lo[i] >> 7) & 0x00FF00FFu);
-        ehi[i] = as_u16x2((hi[i] >> 7) & 0x00FF00FFu);
-    }
-    u16x2 tlo = elo[0], thi = ehi[0], nlo = elo[0], nhi = ehi[0];
+        for (int i = 0; i < TPL; ++i) {
+            const uint16_t* rp = (i == TPL - 1 && grp == NG - 1 && last != nullptr) ? last + c : srow + i * s_p;
+            lo[i] = *reinterpret_cast<const uint32_t*>(rp);
+            hi[i] = *reinterpret_cast<const uint32_t*>(rp + HALF);
+        }
+        u16x2 elo[TPL], ehi[TPL];                  // exponents, one channel per 16-bit lane
 #pragma unroll
-    for (int i = 1; i < 8; ++i) {
-        tlo = vmax(tlo, elo[i]);
-        thi = vmax(thi, ehi[i]);
-        nlo = vmin(nlo, elo[i]);
-        nhi = vmin(nhi, ehi[i]);
-    }
-    tlo = vmax(tlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(tlo), 32)));
-    thi = vmax(thi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(thi), 32)));
-    nlo = vmin(nlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nlo), 32)));
-    nhi = vmin(nhi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nhi), 32)));
-    const u16x2 c15 = {15, 15}, one = {1, 1};
-    const u16x2 flo = vsubs(tlo, c15), fhi = vsubs(thi, c15);                 // floors
-    const u16x2 zlo = vmin(vsubs(one, nlo), vmin(flo, one));                  // zero flags (0 / 1)
-    const u16x2 zhi = vmin(vsubs(one, nhi), vmin(fhi, one));
-    const u16x2 glo = flo + zlo, ghi = fhi + zhi;                             // non-zero e below: raw
-    uint32_t esc = 0;
+        for (int i = 0; i < TPL; ++i) {
+            elo[i] = as_u16x2((lo[i] >> 7) & 0x00FF00FFu);
+            ehi[i] = as_u16x2((hi[i] >> 7) & 0x00FF00FFu);
+        }
+        u16x2 tlo = elo[0], thi = ehi[0], nlo = elo[0], nhi = ehi[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t dlo = as_u32(vmin(vsubs(glo, elo[i]), elo[i]));
-        const uint32_t dhi = as_u32(vmin(vsubs(ghi, ehi[i]), ehi[i]));
-        esc |= (uint32_t)((dlo | dhi) != 0u) << i;
-        // code bytes 2m (nibble of 2m | nibble of 2m+64 << 4) and 2m+1 (2m+1 | 2m+65 << 4)
-        const uint32_t cw = as_u32(vsubs(elo[i], flo)) | (as_u32(vsubs(ehi[i], fhi)) << 4);
-        // sm bytes: sign over bit 7 of each bf16's mantissa byte
-        const uint32_t slo = (lo[i] & 0x007F007Fu) | ((lo[i] >> 8) & 0x00800080u);
-        const uint32_t shi = (hi[i] & 0x007F007Fu) | ((hi[i] >> 8) & 0x00800080u);
-        uint8_t* sp = smrow + i * sm_stride;
-        *reinterpret_cast<uint16_t*>(sp) = bytes02(slo);
-        *reinterpret_cast<uint16_t*>(sp + 64) = bytes02(shi);
-        *reinterpret_cast<uint16_t*>(coderow + i * code_stride) = bytes02(cw);
+        for (int i = 1; i < TPL; ++i) {
+            tlo = vmax(tlo, elo[i]);
+            thi = vmax(thi, ehi[i]);
+            nlo = vmin(nlo, elo[i]);
+            nhi = vmin(nhi, ehi[i]);
+        }
+#pragma unroll
+        for (int d = CL; d < 64; d <<= 1) {
+            tlo = vmax(tlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(tlo), d)));
+            thi = vmax(thi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(thi), d)));
+            nlo = vmin(nlo, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nlo), d)));
+            nhi = vmin(nhi, as_u16x2((uint32_t)__shfl_xor((int)as_u32(nhi), d)));
+        }
+        const u16x2 c15 = {15, 15}, one = {1, 1};
+        const u16x2 flo = vsubs(tlo, c15), fhi = vsubs(thi, c15);                 // floors
+        const u16x2 zlo = vmin(vsubs(one, nlo), vmin(flo, one));                  // zero flags (0 / 1)
+        const u16x2 zhi = vmin(vsubs(one, nhi), vmin(fhi, one));
+        const u16x2 glo = flo + zlo, ghi = fhi + zhi;                             // non-zero e below: raw
+#pragma unroll
+        for (int i = 0; i < TPL; ++i) {
+            const uint32_t dlo = as_u32(vmin(vsubs(glo, elo[i]), elo[i]));
+            const uint32_t dhi = as_u32(vmin(vsubs(ghi, ehi[i]), ehi[i]));
+            esc |= (uint32_t)((dlo | dhi) != 0u) << i;
+            // code bytes c (nibble of c | nibble of c+D/2 << 4) and c+1 (c+1 | c+1+D/2 << 4)
+            const uint32_t cw = as_u32(vsubs(elo[i], flo)) | (as_u32(vsubs(ehi[i], fhi)) << 4);
+            // sm bytes: sign over bit 7 of each bf16's mantissa byte
+            const uint32_t slo = (lo[i] & 0x007F007Fu) | ((lo[i] >> 8) & 0x00800080u);
+            const uint32_t shi = (hi[i] & 0x007F007Fu) | ((hi[i] >> 8) & 0x00800080u);
+            uint8_t* sp = smrow + i * sm_stride;
+            *reinterpret_cast<uint16_t*>(sp) = bytes02(slo);
+            *reinterpret_cast<uint16_t*>(sp + HALF) = bytes02(shi);
+            *reinterpret_cast<uint16_t*>(coderow + i * code_stride) = bytes02(cw);
+        }
+        if (grp == 0) {
+            const u16x2 c128 = {128, 128}, c255 = {255, 255};
+            const uint32_t blo = as_u32(vmin(flo + zlo * c128, c255)), bhi = as_u32(vmin(fhi + zhi * c128, c255));
+            *reinterpret_cast<uint16_t*>(basep + c) = bytes02(blo);
+            *reinterpret_cast<uint16_t*>(basep + HALF + c) = bytes02(bhi);
+        }
+        big = big || ((as_u32(flo) | as_u32(fhi)) & 0xFF80FF80u) != 0u;
     }
-    if (half == 0) {
-        const u16x2 c128 = {128, 128}, c255 = {255, 255};
-        const uint32_t blo = as_u32(vmin(flo + zlo * c128, c255)), bhi = as_u32(vmin(fhi + zhi * c128, c255));
-        *reinterpret_cast<uint16_t*>(basep + 2 * m) = bytes02(blo);
-        *reinterpret_cast<uint16_t*>(basep + 64 + 2 * m) = bytes02(bhi);
-    }
-    // rowmask: ballot bit l < 32 is token i (half 0), bit 32 + l token 8 + i; a floor of
-    // 128 or more in any channel makes every row raw
-    const bool big = ((as_u32(flo) | as_u32(fhi)) & 0xFF80FF80u) != 0u;
+    // rowmask: ballot bits [CL*grp, CL*grp + CL) are token TPL*grp + i; a floor of 128 or
+    // more in any channel makes every row raw
     uint32_t rm = __ballot(big) != 0 ? 0xFFFFu : 0u;
+    constexpr uint64_t kGroup = CL == 64 ? ~0ull : (1ull << CL) - 1ull;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < TPL; ++i) {
         const uint64_t bal = __ballot((esc >> i) & 1u);
-        if ((uint32_t)bal != 0u) rm |= 1u << i;
-        if ((uint32_t)(bal >> 32) != 0u) rm |= 1u << (8 + i);
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi)
+            if (((bal >> (CL * gi)) & kGroup) != 0u) rm |= 1u << (TPL * gi + i);
     }
     if (lane == 0) *rmaskp = (int32_t)rm;
 }
@@ -143,6 +164,7 @@ struct EncArgs {
     const int32_t* dst_pages = nullptr;
     int64_t dst_stride = 0;
     int64_t all_pages = 0;
+    int D = kD;                       // head dim: 64, 128 or 256
 };
 
 __device__ inline void unit_coords(const EncArgs& a, int64_t u, int& bi, int& pg, int& hk) {
@@ -164,6 +186,7 @@ __device__ inline int64_t unit_page(const EncArgs& a, int bi, int pg, int hk) {
 
 // One wavefront per unit (sequence, page, head); the unit's coordinates and addresses are
 // wavefront-uniform (scalar arithmetic, 32-bit: unit counts are below 2^31).
+template <int D>
 __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int nunits) {
     const int lane = threadIdx.x & 63;
     const int u = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -173,8 +196,8 @@ __global__ void __launch_bounds__(256) enc_pages_kernel(EncArgs a, int nunits) {
     const uint16_t* src = a.src + (int64_t)bi * a.s_b + (int64_t)pg * a.s_pg + (int64_t)hk * a.s_h;
     const int64_t pidx = unit_pidx(a, (int)bi, pg);
     const int64_t row0 = pidx * kPage * a.H + hk, page = pidx * a.H + hk;
-    encode_page(src, a.s_p, nullptr, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
-                a.rowmask + page);
+    encode_page<D>(src, a.s_p, nullptr, lane, a.sm + row0 * D, a.code + row0 * (D / 2), a.H, a.base + page * D,
+                   a.rowmask + page);
 }
 
 // The slot scan after a page encode, one unit per thread and 1024 units per block, every
@@ -240,16 +263,19 @@ __global__ void __launch_bounds__(1024) scan_blocks_kernel(EncArgs a, int64_t nb
     }
 }
 
-// The raw rows of the escaped units among a wavefront's 64 (lane = unit: mask m, first slot
-// off, source row 0 at src). VEC16 (source rows 16-byte aligned): four units at a time, a
-// 16-lane group per unit, each lane moving 16 bytes of every row of its unit with all the
-// unit's loads in flight; else one unit at a time, 4 bytes of each row per lane. Slots at
+// The raw rows (D channels) of the escaped units among a wavefront's 64 (lane = unit: mask
+// m, first slot off, source row 0 at src). VEC16 (source rows 16-byte aligned): four units
+// at a time, a 16-lane group per unit, each lane moving D/16 channels (8 or 16 bytes) of
+// every row of its unit per pass (two passes for D = 256) with all the unit's loads of a
+// pass in flight; else one unit at a time, 4 bytes of each row per lane per pass. Slots at
 // or past cap are skipped (the host grows the pool and encodes again).
-template <bool VEC16>
+template <bool VEC16, int D>
 __device__ inline void copy_escaped_rows(const EncArgs& a, uint32_t m, int32_t off, const uint16_t* src,
                                          int lane) {
     uint64_t todo = __ballot(m != 0);
     if (VEC16) {
+        constexpr int EPL = D == 64 ? 4 : 8;           // channels per lane per pass
+        constexpr int NPASS = D / (16 * EPL);
         const int g = lane >> 4, j = lane & 15;
         while (todo != 0) {
             int pick = -1;                             // group g takes the g-th unit left
@@ -267,22 +293,31 @@ __device__ inline void copy_escaped_rows(const EncArgs& a, uint32_t m, int32_t o
             const int32_t op = __shfl(off, from);
             const uint64_t sp = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(uintptr_t)src, from)) |
                                 ((uint64_t)(uint32_t)__shfl((int)(uint32_t)((uintptr_t)src >> 32), from) << 32);
-            const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + 8 * j;
             const int nr = popc32(mp);
-            uint32_t t = mp;
-            uint4 r[kPage];
 #pragma unroll
-            for (int k = 0; k < kPage; ++k) {          // the k-th escaped row of the unit
-                const int p = t != 0u ? __builtin_ctz(t) : 0;
-                t &= t - 1u;
-                r[k] = k < nr ? *reinterpret_cast<const uint4*>(s + p * a.s_p) : uint4{0u, 0u, 0u, 0u};
+            for (int pass = 0; pass < NPASS; ++pass) {
+                const int c0 = 16 * EPL * pass + EPL * j;
+                const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + c0;
+                uint32_t t = mp;
+                uint32_t r[kPage][EPL / 2];
+#pragma unroll
+                for (int k = 0; k < kPage; ++k) {      // the k-th escaped row of the unit
+                    const int p = t != 0u ? __builtin_ctz(t) : 0;
+                    t &= t - 1u;
+                    if (k < nr) {
+                        ld_words<EPL / 2>(s + p * a.s_p, r[k]);
+                    } else {
+#pragma unroll
+                        for (int w = 0; w < EPL / 2; ++w) r[k][w] = 0u;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < kPage; ++k)
+                    if (k < nr && (int64_t)op + k < a.cap) st_words<EPL / 2>(a.raw + ((int64_t)op + k) * D + c0, r[k]);
             }
-#pragma unroll
-            for (int k = 0; k < kPage; ++k)
-                if (k < nr && (int64_t)op + k < a.cap)
-                    *reinterpret_cast<uint4*>(a.raw + ((int64_t)op + k) * 128 + 8 * j) = r[k];
         }
     } else {
+        constexpr int NPASS = D > 128 ? D / 128 : 1;
         while (todo != 0) {
             const int l = __builtin_ctzll(todo);
             todo &= todo - 1;
@@ -290,25 +325,30 @@ __device__ inline void copy_escaped_rows(const EncArgs& a, uint32_t m, int32_t o
             const int32_t op = __builtin_amdgcn_readlane(off, l);
             const uint64_t sp = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(uintptr_t)src, l) |
                                 ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uintptr_t)src >> 32), l) << 32);
-            const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + 2 * lane;
             const int nr = popc32(mp);
-            uint32_t t = mp;
-            uint32_t r[kPage];
 #pragma unroll
-            for (int k = 0; k < kPage; ++k) {
-                const int p = t != 0u ? __builtin_ctz(t) : 0;
-                t &= t - 1u;
-                r[k] = k < nr ? *reinterpret_cast<const uint32_t*>(s + p * a.s_p) : 0u;
+            for (int pass = 0; pass < NPASS; ++pass) {
+                const int c0 = 128 * pass + 2 * lane;
+                if (c0 >= D) continue;                 // D = 64: half the lanes
+                const uint16_t* s = reinterpret_cast<const uint16_t*>(sp) + c0;
+                uint32_t t = mp;
+                uint32_t r[kPage];
+#pragma unroll
+                for (int k = 0; k < kPage; ++k) {
+                    const int p = t != 0u ? __builtin_ctz(t) : 0;
+                    t &= t - 1u;
+                    r[k] = k < nr ? *reinterpret_cast<const uint32_t*>(s + p * a.s_p) : 0u;
+                }
+#pragma unroll
+                for (int k = 0; k < kPage; ++k)
+                    if (k < nr && (int64_t)op + k < a.cap)
+                        *reinterpret_cast<uint32_t*>(a.raw + ((int64_t)op + k) * D + c0) = r[k];
             }
-#pragma unroll
-            for (int k = 0; k < kPage; ++k)
-                if (k < nr && (int64_t)op + k < a.cap)
-                    *reinterpret_cast<uint32_t*>(a.raw + ((int64_t)op + k) * 128 + 2 * lane) = r[k];
         }
     }
 }
 
-template <bool PAGED, bool VEC16>
+template <bool PAGED, bool VEC16, int D>
 __global__ void __launch_bounds__(1024) scan_write_kernel(EncArgs a, int nunits) {
     __shared__ int s_base;
     if (threadIdx.x == 0) s_base = a.rowoff[first_page_of(a, blockIdx.x)];
@@ -323,9 +363,10 @@ __global__ void __launch_bounds__(1024) scan_write_kernel(EncArgs a, int nunits)
     int total;
     const int off = block_excl_scan(popc32(m), total) + s_base;   // synchronises: s_base is read
     if (u < nunits) a.rowoff[page] = off;
-    copy_escaped_rows<VEC16>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, threadIdx.x & 63);
+    copy_escaped_rows<VEC16, D>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, threadIdx.x & 63);
 }
 
+template <int D>
 static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
     const unsigned nb = (unsigned)((n + kScanUnits - 1) / kScanUnits);
     const bool paged = a.dst_pages != nullptr;
@@ -336,8 +377,8 @@ static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
     else
         hipLaunchKernelGGL(scan_count_kernel<false>, dim3(nb), dim3(1024), 0, stream, a, (int)n);
     hipLaunchKernelGGL(scan_blocks_kernel, dim3(1), dim3(1024), 0, stream, a, (int64_t)nb);
-    auto k = paged ? (vec16 ? scan_write_kernel<true, true> : scan_write_kernel<true, false>)
-                   : (vec16 ? scan_write_kernel<false, true> : scan_write_kernel<false, false>);
+    auto k = paged ? (vec16 ? scan_write_kernel<true, true, D> : scan_write_kernel<true, false, D>)
+                   : (vec16 ? scan_write_kernel<false, true, D> : scan_write_kernel<false, false, D>);
     hipLaunchKernelGGL(k, dim3(nb), dim3(1024), 0, stream, a, (int)n);
 }
 
@@ -395,7 +436,7 @@ __device__ inline int64_t chain_lookback(const uint64_t* ws, uint32_t tag, int t
     return excl;
 }
 
-template <bool PAGED, bool VEC16>
+template <bool PAGED, bool VEC16, int D>
 __global__ void __launch_bounds__(1024) scan_chain_kernel(EncArgs a, int nunits, int nblocks, uint64_t* ws) {
     __shared__ int s_tile, s_excl;
     __shared__ uint32_t s_gen;
@@ -444,27 +485,38 @@ __global__ void __launch_bounds__(1024) scan_chain_kernel(EncArgs a, int nunits,
     __syncthreads();
     const int off = s_excl + pre;
     if (u < nunits) a.rowoff[page] = off;
-    copy_escaped_rows<VEC16>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, lane);
+    copy_escaped_rows<VEC16, D>(a, m, off, a.src + bi * a.s_b + pg * a.s_pg + hk * a.s_h, lane);
 }
 
 // Encode n units: the page kernel, then the chained scan when the workspace has at least
 // 2 + ceil(n / kScanUnits) words, else the three-launch scan.
-static void launch_encode(const EncArgs& a, int64_t n, uint64_t* ws, int64_t ws_words, hipStream_t stream) {
-    hipLaunchKernelGGL(enc_pages_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a, (int)n);
+template <int D>
+static void launch_encode_d(const EncArgs& a, int64_t n, uint64_t* ws, int64_t ws_words, hipStream_t stream) {
+    hipLaunchKernelGGL(enc_pages_kernel<D>, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a, (int)n);
     const int64_t nb = (n + kScanUnits - 1) / kScanUnits;
     if (ws == nullptr || ws_words < 2 + nb) {
-        launch_scan(a, n, stream);
+        launch_scan<D>(a, n, stream);
         return;
     }
     const bool paged = a.dst_pages != nullptr;
     const bool vec16 = (uintptr_t)a.src % 16 == 0 && a.s_b % 8 == 0 && a.s_pg % 8 == 0 && a.s_p % 8 == 0 &&
                        a.s_h % 8 == 0;
-    auto k = paged ? (vec16 ? scan_chain_kernel<true, true> : scan_chain_kernel<true, false>)
-                   : (vec16 ? scan_chain_kernel<false, true> : scan_chain_kernel<false, false>);
+    auto k = paged ? (vec16 ? scan_chain_kernel<true, true, D> : scan_chain_kernel<true, false, D>)
+                   : (vec16 ? scan_chain_kernel<false, true, D> : scan_chain_kernel<false, false, D>);
     hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(kScanUnits), 0, stream, a, (int)n, (int)nb, ws);
 }
 
-// Copy one page's raw rows (token p's row at src + p*s_p) into slots rowoff + k (< cap).
+static void launch_encode(const EncArgs& a, int64_t n, uint64_t* ws, int64_t ws_words, hipStream_t stream) {
+    if (a.D == 64)
+        launch_encode_d<64>(a, n, ws, ws_words, stream);
+    else if (a.D == 256)
+        launch_encode_d<256>(a, n, ws, ws_words, stream);
+    else
+        launch_encode_d<128>(a, n, ws, ws_words, stream);
+}
+
+// Copy one page's raw rows (token p's row at src + p*s_p, D channels) into slots rowoff + k (< cap).
+template <int D>
 __device__ inline void copy_raw_rows(const uint16_t* src, int64_t s_p, uint32_t m, int32_t off, int64_t cap,
                                      uint16_t* raw, int lane) {
     int k = 0;
@@ -473,16 +525,23 @@ __device__ inline void copy_raw_rows(const uint16_t* src, int64_t s_p, uint32_t 
         const int64_t slot = (int64_t)off + k++;
         if (slot >= cap) continue;
         const uint16_t* s = src + p * s_p;
-        uint16_t* d = raw + slot * 128;
-        d[lane] = s[lane];
-        d[lane + 64] = s[lane + 64];
+        uint16_t* d = raw + slot * D;
+#pragma unroll
+        for (int c = 0; c < D; c += 64) d[c + lane] = s[c + lane];
     }
+}
+
+// Row of D channels: d[c] = s[c], lanes striding by 64.
+template <int D>
+__device__ inline void copy_row(uint16_t* d, const uint16_t* s, int lane) {
+#pragma unroll
+    for (int c = 0; c < D; c += 64) d[c + lane] = s[c + lane];
 }
 
 // ---------------------------------------------------------------- device-side append
 
 struct AppendArgs {
-    const uint16_t* x;        // [B, H, 128] (row strides sx_b, sx_h in elements)
+    const uint16_t* x;        // [B, H, D] (row strides sx_b, sx_h in elements)
     int64_t sx_b, sx_h;
     uint8_t* sm;
     uint8_t* code;
@@ -499,6 +558,7 @@ struct AppendArgs {
 
 // Writes the new token into the tail area; when it completes a page, encodes that page
 // and opens the next one (rowmask all ones, rowoff into the tail area).
+template <int D>
 __global__ void __launch_bounds__(256) append_write_kernel(AppendArgs a) {
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -507,17 +567,16 @@ __global__ void __launch_bounds__(256) append_write_kernel(AppendArgs a) {
     const int T = a.state[0];
     if (T < 0 || T >= a.TS) return;                // full cache: nothing is written
     const int p = T % kPage;
-    uint16_t* tail = a.raw + (a.cap + (int64_t)u * kPage) * 128;
+    uint16_t* tail = a.raw + (a.cap + (int64_t)u * kPage) * D;
     const uint16_t* x = a.x + b * a.sx_b + h * a.sx_h;
-    tail[p * 128 + lane] = x[lane];
-    tail[p * 128 + lane + 64] = x[lane + 64];
+    copy_row<D>(tail + p * D, x, lane);
     if (p != kPage - 1) return;
     const int NP = a.TS / kPage;
     const int pg = T / kPage;
     const int64_t row0 = ((int64_t)b * a.TS + (int64_t)pg * kPage) * a.H + h;
     const int64_t page = ((int64_t)b * NP + pg) * a.H + h;
-    encode_page(tail, 128, x, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
-                a.rowmask + page);
+    encode_page<D>(tail, D, x, lane, a.sm + row0 * D, a.code + row0 * (D / 2), a.H, a.base + page * D,
+                   a.rowmask + page);
     if (pg + 1 < NP && lane == 0) {
         a.rowmask[page + a.H] = 0xFFFF;
         a.rowoff[page + a.H] = (int32_t)(a.cap + (int64_t)u * kPage);
@@ -552,6 +611,7 @@ __global__ void __launch_bounds__(1024) append_scan_kernel(AppendArgs a) {
     if (threadIdx.x == 0) a.state[0] = T + 1;
 }
 
+template <int D>
 __global__ void __launch_bounds__(256) append_rawcopy_kernel(AppendArgs a) {
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -562,10 +622,11 @@ __global__ void __launch_bounds__(256) append_rawcopy_kernel(AppendArgs a) {
     const int64_t page = ((int64_t)(u / a.H) * NP + pg) * a.H + u % a.H;
     const uint32_t m = (uint32_t)a.rowmask[page];
     if (m == 0) return;
-    copy_raw_rows(a.raw + (a.cap + (int64_t)u * kPage) * 128, 128, m, a.rowoff[page], a.cap, a.raw, lane);
+    copy_raw_rows<D>(a.raw + (a.cap + (int64_t)u * kPage) * D, D, m, a.rowoff[page], a.cap, a.raw, lane);
 }
 
 // Plain bf16 cache (reference cache.py:129-146): buf[b, T, h] = x[b, h], T from device.
+template <int D>
 __global__ void __launch_bounds__(256) bf16_append_kernel(const uint16_t* x, int64_t sx_b, int64_t sx_h,
                                                           uint16_t* buf, const int32_t* state, int B, int H,
                                                           int TS) {
@@ -575,10 +636,7 @@ __global__ void __launch_bounds__(256) bf16_append_kernel(const uint16_t* x, int
     const int T = state[0];
     if (T < 0 || T >= TS) return;
     const int b = u / H, h = u % H;
-    uint16_t* d = buf + (((int64_t)b * TS + T) * H + h) * 128;
-    const uint16_t* s = x + b * sx_b + h * sx_h;
-    d[lane] = s[lane];
-    d[lane + 64] = s[lane + 64];
+    copy_row<D>(buf + (((int64_t)b * TS + T) * H + h) * D, x + b * sx_b + h * sx_h, lane);
 }
 
 __global__ void bump_kernel(int32_t* state, int TS) {
@@ -625,7 +683,7 @@ __global__ void __launch_bounds__(256) open_pages_paged_kernel(int32_t* rowmask,
 // held in the tail area at raw rows cap + (s * H + h) * 16; when the new token fills it,
 // the page is encoded into its pool page and the next table entry is opened.
 struct PagedAppendArgs {
-    const uint16_t* x;        // [n, H, 128] (row strides sx_b, sx_h in elements)
+    const uint16_t* x;        // [n, H, D] (row strides sx_b, sx_h in elements)
     int64_t sx_b, sx_h;
     uint8_t* sm;
     uint8_t* code;
@@ -655,6 +713,7 @@ __device__ inline int paged_new_token(const PagedAppendArgs& a, int s) {
     return (T >= 0 && T < a.max_pages * kPage) ? T : -1;
 }
 
+template <int D>
 __global__ void __launch_bounds__(256) paged_append_write_kernel(PagedAppendArgs a) {
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -665,17 +724,16 @@ __global__ void __launch_bounds__(256) paged_append_write_kernel(PagedAppendArgs
     if (T < 0) return;
     const int p = T % kPage;
     const int64_t tslot = a.cap + ((int64_t)s * a.H + h) * kPage;
-    uint16_t* tail = a.raw + tslot * 128;
+    uint16_t* tail = a.raw + tslot * D;
     const uint16_t* x = a.x + i * a.sx_b + h * a.sx_h;
-    tail[p * 128 + lane] = x[lane];
-    tail[p * 128 + lane + 64] = x[lane + 64];
+    copy_row<D>(tail + p * D, x, lane);
     if (p != kPage - 1) return;
     const int pg = T / kPage;
     const int64_t pidx = paged_pidx(a, s, pg);
     const int64_t row0 = pidx * kPage * a.H + h;
     const int64_t page = pidx * a.H + h;
-    encode_page(tail, 128, x, lane, a.sm + row0 * 128, a.code + row0 * 64, a.H, a.base + page * 128,
-                a.rowmask + page);
+    encode_page<D>(tail, D, x, lane, a.sm + row0 * D, a.code + row0 * (D / 2), a.H, a.base + page * D,
+                   a.rowmask + page);
     if (pg + 1 < a.max_pages && lane == 0) {
         const int64_t next = paged_pidx(a, s, pg + 1) * a.H + h;
         a.rowmask[next] = 0xFFFF;
@@ -715,6 +773,7 @@ __global__ void __launch_bounds__(1024) paged_append_scan_kernel(PagedAppendArgs
     }
 }
 
+template <int D>
 __global__ void __launch_bounds__(256) paged_append_rawcopy_kernel(PagedAppendArgs a) {
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -726,11 +785,12 @@ __global__ void __launch_bounds__(256) paged_append_rawcopy_kernel(PagedAppendAr
     const int64_t page = paged_pidx(a, s, T / kPage) * a.H + h;
     const uint32_t m = (uint32_t)a.rowmask[page];
     if (m == 0) return;
-    copy_raw_rows(a.raw + (a.cap + ((int64_t)s * a.H + h) * kPage) * 128, 128, m, a.rowoff[page], a.cap, a.raw,
-                  lane);
+    copy_raw_rows<D>(a.raw + (a.cap + ((int64_t)s * a.H + h) * kPage) * D, D, m, a.rowoff[page], a.cap, a.raw,
+                     lane);
 }
 
 // bf16 twin: pool[(page * 16 + T % 16) * H + h] = x[i, h], page = bt[s, T / 16].
+template <int D>
 __global__ void __launch_bounds__(256) paged_bf16_append_kernel(PagedAppendArgs a, uint16_t* buf) {
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -740,17 +800,14 @@ __global__ void __launch_bounds__(256) paged_bf16_append_kernel(PagedAppendArgs 
     const int T = paged_new_token(a, s);
     if (T < 0) return;
     const int64_t row = paged_pidx(a, s, T / kPage) * kPage + T % kPage;
-    uint16_t* d = buf + (row * a.H + h) * 128;
-    const uint16_t* x = a.x + i * a.sx_b + h * a.sx_h;
-    d[lane] = x[lane];
-    d[lane + 64] = x[lane + 64];
+    copy_row<D>(buf + (row * a.H + h) * D, a.x + i * a.sx_b + h * a.sx_h, lane);
 }
 
 // ---------------------------------------------------------------- decode to bf16
 
 struct DecArgs {
     CSrc c;
-    uint16_t* out;            // [B, T, H, 128]
+    uint16_t* out;            // [B, T, H, D]
     int B, T, TS, H;
     // paged: page pg of sequence b is pool page bt[b * bt_stride + pg] (clamped to pool_pages)
     const int32_t* bt = nullptr;
@@ -758,8 +815,11 @@ struct DecArgs {
     int64_t pool_pages = 0;
 };
 
-// One wavefront per (sequence, page, head), through the attention kernels' page decoder.
+// One wavefront per (sequence, page, head), lane = (token r, channel group g): the page
+// rebuild of the attention kernels (tile.hpp), any head dim.
+template <int D>
 __global__ void __launch_bounds__(256) decode_kernel(DecArgs a) {
+    constexpr int R = Run<D>::R;
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const int NP = a.TS / kPage;
     const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -771,16 +831,30 @@ __global__ void __launch_bounds__(256) decode_kernel(DecArgs a) {
     const int t = pg * kPage + r;
     const int64_t pidx = a.bt ? (int64_t)min((uint32_t)a.bt[b * a.bt_stride + pg], (uint32_t)(a.pool_pages - 1))
                               : (int64_t)b * NP + pg;
-    PageBytes pb;
-    load_page(a.c, (pidx * kPage + r) * a.H + h, pidx * a.H + h, g, pb);
-    uint32_t v[16];
-    rebuild_page(a.c, pb, r, g, v);
+    const int64_t page = pidx * a.H + h;
+    PageBytesD<D> pb;
+    load_page_d<D>(a.c, (pidx * kPage + r) * a.H + h, page, g, pb);
+    const uint32_t rmask = (uint32_t)a.c.rowmask[page];
+    const int32_t roff = a.c.rowoff[page];
+    uint32_t v[Run<D>::V];
+    rebuild_page_d<D>(a.c, pb, rmask, roff, r, g, v);
     if (t >= a.T) return;
-    uint4* o = reinterpret_cast<uint4*>(a.out + (((int64_t)b * a.T + t) * a.H + h) * 128 + 16 * g);
-    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
-    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
-    o[8] = make_uint4(v[8], v[9], v[10], v[11]);
-    o[9] = make_uint4(v[12], v[13], v[14], v[15]);
+    uint16_t* o = a.out + (((int64_t)b * a.T + t) * a.H + h) * D + g * R;
+    st_words<R / 2>(o, v);
+    st_words<R / 2>(o + D / 2, v + R / 2);
+}
+
+template <int D>
+static void launch_decode(const DecArgs& a, int64_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(decode_kernel<D>, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a);
+}
+static void launch_decode_any(int D, const DecArgs& a, int64_t n, hipStream_t stream) {
+    if (D == 64)
+        launch_decode<64>(a, n, stream);
+    else if (D == 256)
+        launch_decode<256>(a, n, stream);
+    else
+        launch_decode<128>(a, n, stream);
 }
 
 }  // namespace exkv
@@ -789,12 +863,15 @@ using namespace exkv;
 
 static int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
 
+// The instance of kernel template K for head dim D (64, 128 or 256; checked by the caller).
+#define EXKV_FOR_D(K, D) ((D) == 64 ? K<64> : (D) == 256 ? K<256> : K<128>)
+
 extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int64_t s_p, int64_t s_h,
                                  void* sm, void* code, void* base, int32_t* rowmask, int32_t* rowoff, void* raw,
                                  int32_t* cnt, int32_t* before, int64_t cap, int64_t raw_rows, int32_t B,
                                  int32_t b0, int32_t pg0, int32_t nb, int32_t npg, int32_t H, int32_t TS,
                                  int32_t D, void* scan_ws, int64_t scan_ws_words, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "encode_pages: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "encode_pages: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages: TS must be a positive multiple of 16 (got %d)", TS);
     EXKV_REQUIRE(H > 0 && B > 0, "encode_pages: bad H=%d or B=%d", H, B);
     EXKV_REQUIRE(nb >= 0 && npg >= 0 && b0 >= 0 && pg0 >= 0, "encode_pages: negative range");
@@ -813,6 +890,7 @@ extern "C" int exkv_encode_pages(const void* src, int64_t s_b, int64_t s_pg, int
     EXKV_REQUIRE(scan_ws == nullptr || (uintptr_t)scan_ws % 8 == 0, "encode_pages: scan workspace must be 8-byte aligned");
     EncArgs a{(const uint16_t*)src, s_b, s_pg, s_p, s_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base,
               rowmask, rowoff, (uint16_t*)raw, cnt, before, cap, b0, pg0, nb, npg, H, TS};
+    a.D = D;
     launch_encode(a, n, (uint64_t*)scan_ws, scan_ws_words, stream);
     return launch_status("encode_pages");
 }
@@ -827,7 +905,7 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
                                        int32_t B, const int32_t* dst_pages, int64_t dst_stride, int32_t nb,
                                        int32_t npg, int32_t H, int32_t TS, int32_t D, void* scan_ws,
                                        int64_t scan_ws_words, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "encode_pages_paged: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "encode_pages_paged: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0, "encode_pages_paged: TS must be a positive multiple of 16 (got %d)", TS);
     EXKV_REQUIRE(H > 0 && B > 0, "encode_pages_paged: bad H=%d or B=%d", H, B);
     EXKV_REQUIRE(nb >= 0 && npg >= 0, "encode_pages_paged: negative range");
@@ -846,6 +924,7 @@ extern "C" int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_p
     a.dst_pages = dst_pages;
     a.dst_stride = dst_stride;
     a.all_pages = (int64_t)B * (TS / kPage);
+    a.D = D;
     EXKV_REQUIRE(scan_ws == nullptr || (uintptr_t)scan_ws % 8 == 0,
                  "encode_pages_paged: scan workspace must be 8-byte aligned");
     launch_encode(a, n, (uint64_t*)scan_ws, scan_ws_words, stream);
@@ -856,7 +935,7 @@ extern "C" int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void
                                  int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,
                                  int32_t* state, int64_t cap, int64_t raw_rows, int32_t B, int32_t H,
                                  int32_t TS, int32_t D, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "append: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "append: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0 && B > 0 && H > 0, "append: bad shape B=%d H=%d TS=%d", B, H, TS);
     EXKV_REQUIRE(cap >= 0 && cap + (int64_t)B * H * kPage <= raw_rows,
                  "append: raw pool (%lld rows) smaller than cap + tail area", (long long)raw_rows);
@@ -867,18 +946,18 @@ extern "C" int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void
     AppendArgs a{(const uint16_t*)x, sx_b, sx_h, (uint8_t*)sm, (uint8_t*)code, (uint8_t*)base, rowmask, rowoff,
                  (uint16_t*)raw, cnt, before, state, cap, B, H, TS};
     const unsigned grid = (unsigned)((B * H + 3) / 4);
-    hipLaunchKernelGGL(append_write_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(EXKV_FOR_D(append_write_kernel, D), dim3(grid), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(append_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
-    hipLaunchKernelGGL(append_rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(EXKV_FOR_D(append_rawcopy_kernel, D), dim3(grid), dim3(256), 0, stream, a);
     return launch_status("cache_append");
 }
 
 extern "C" int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void* buf, int32_t* state,
                                 int32_t B, int32_t H, int32_t TS, int32_t D, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "bf16_append: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "bf16_append: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(B > 0 && H > 0 && TS > 0, "bf16_append: bad shape");
     EXKV_REQUIRE(x && buf && state, "bf16_append: null pointer");
-    hipLaunchKernelGGL(bf16_append_kernel, dim3((unsigned)((B * H + 3) / 4)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(EXKV_FOR_D(bf16_append_kernel, D), dim3((unsigned)((B * H + 3) / 4)), dim3(256), 0, stream,
                        (const uint16_t*)x, sx_b, sx_h, (uint16_t*)buf, (const int32_t*)state, B, H, TS);
     hipLaunchKernelGGL(bump_kernel, dim3(1), dim3(1), 0, stream, state, TS);
     return launch_status("bf16_append");
@@ -914,7 +993,7 @@ extern "C" int exkv_cache_open_pages_paged(int32_t* rowmask, int32_t* rowoff, co
 
 static int check_paged_append(const char* what, int32_t n, int32_t H, int32_t D, int32_t max_seqs,
                               int32_t max_pages, int64_t bt_stride, int32_t pool_pages) {
-    EXKV_REQUIRE(D == kD, "%s: head dim must be 128 (got %d)", what, D);
+    EXKV_REQUIRE(head_dim_ok(D), "%s: head dim must be 64, 128 or 256 (got %d)", what, D);
     EXKV_REQUIRE(n >= 0 && H > 0 && max_seqs > 0 && n <= max_seqs, "%s: bad shape n=%d H=%d max_seqs=%d", what, n,
                  H, max_seqs);
     EXKV_REQUIRE(max_pages > 0 && bt_stride >= max_pages && pool_pages > 0,
@@ -942,9 +1021,9 @@ extern "C" int exkv_cache_append_paged(const void* x, int64_t sx_b, int64_t sx_h
                       rowoff, (uint16_t*)raw, cnt, before, slots, lens, block_table, bt_stride, cap, n, H,
                       max_seqs, max_pages, pool_pages};
     const unsigned grid = (unsigned)((n * H + 3) / 4);
-    hipLaunchKernelGGL(paged_append_write_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(EXKV_FOR_D(paged_append_write_kernel, D), dim3(grid), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(paged_append_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
-    hipLaunchKernelGGL(paged_append_rawcopy_kernel, dim3(grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(EXKV_FOR_D(paged_append_rawcopy_kernel, D), dim3(grid), dim3(256), 0, stream, a);
     return launch_status("cache_append_paged");
 }
 
@@ -959,8 +1038,8 @@ extern "C" int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h,
     PagedAppendArgs a{(const uint16_t*)x, sx_b, sx_h, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                       nullptr, nullptr, slots, lens, block_table, bt_stride, 0, n, H, max_seqs, max_pages,
                       pool_pages};
-    hipLaunchKernelGGL(paged_bf16_append_kernel, dim3((unsigned)((n * H + 3) / 4)), dim3(256), 0, stream, a,
-                       (uint16_t*)buf);
+    hipLaunchKernelGGL(EXKV_FOR_D(paged_bf16_append_kernel, D), dim3((unsigned)((n * H + 3) / 4)), dim3(256), 0,
+                       stream, a, (uint16_t*)buf);
     return launch_status("bf16_append_paged");
 }
 
@@ -969,7 +1048,7 @@ extern "C" int exkv_decode_to_bf16_paged(const void* sm, const void* code, const
                                          int64_t raw_rows, int64_t pool_pages, const int32_t* block_table,
                                          int64_t bt_stride, void* out, int32_t B, int32_t T, int32_t H, int32_t D,
                                          hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "decode_to_bf16_paged: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "decode_to_bf16_paged: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(B > 0 && H > 0 && bt_stride > 0 && pool_pages > 0, "decode_to_bf16_paged: bad shape");
     EXKV_REQUIRE(T >= 0 && T <= bt_stride * kPage, "decode_to_bf16_paged: T=%d exceeds the table's %lld pages", T,
                  (long long)bt_stride);
@@ -984,15 +1063,14 @@ extern "C" int exkv_decode_to_bf16_paged(const void* sm, const void* code, const
     a.bt = block_table;
     a.bt_stride = bt_stride;
     a.pool_pages = pool_pages;
-    const int64_t n = (int64_t)B * (TS / kPage) * H;
-    hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a);
+    launch_decode_any(D, a, (int64_t)B * (TS / kPage) * H, stream);
     return launch_status("decode_to_bf16_paged");
 }
 
 extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,
                                    const int32_t* rowoff, const void* raw, int64_t raw_rows, void* out,
                                    int32_t B, int32_t T, int32_t TS, int32_t H, int32_t D, hipStream_t stream) {
-    EXKV_REQUIRE(D == kD, "decode_to_bf16: head dim must be 128 (got %d)", D);
+    EXKV_REQUIRE(head_dim_ok(D), "decode_to_bf16: head dim must be 64, 128 or 256 (got %d)", D);
     EXKV_REQUIRE(TS > 0 && TS % kPage == 0 && B > 0 && H > 0, "decode_to_bf16: bad shape");
     EXKV_REQUIRE(T >= 0 && T <= TS, "decode_to_bf16: T=%d outside [0, TS=%d]", T, TS);
     EXKV_REQUIRE(raw_rows > 0, "decode_to_bf16: empty raw pool");
@@ -1001,7 +1079,6 @@ extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void*
     DecArgs a{CSrc{(const uint8_t*)sm, (const uint8_t*)code, (const uint8_t*)base, rowmask, rowoff,
                    (const uint16_t*)raw, raw_rows},
               (uint16_t*)out, B, T, TS, H};
-    const int64_t n = (int64_t)B * (TS / kPage) * H;
-    hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, a);
+    launch_decode_any(D, a, (int64_t)B * (TS / kPage) * H, stream);
     return launch_status("decode_to_bf16");
 }

@@ -52,18 +52,18 @@ extern "C" int exkv_attn_compressed_noalloc(const void* q, const void* k_sm, con
                                             int32_t Hkv, int32_t D, int32_t T, int32_t TS, const int32_t* lens,
                                             int64_t lens_stride, int32_t nsplit, int32_t split_len, int32_t window,
                                             float qk_scale, hipStream_t stream) {
-    EXKV_REQUIRE(B > 0 && Hq > 0 && nsplit > 0 && D == 128,
+    EXKV_REQUIRE(B > 0 && Hq > 0 && nsplit > 0 && exkv::head_dim_ok(D),
                  "attn_compressed_noalloc: bad shape B=%d Hq=%d nsplit=%d D=%d", B, Hq, nsplit, D);
     const int64_t partials = (int64_t)B * Hq * nsplit;             // (sequence, query head, split)
-    const int64_t need = partials * (128 + 2) * (int64_t)sizeof(float);
+    const int64_t need = partials * (D + 2) * (int64_t)sizeof(float);
     EXKV_REQUIRE(need <= exkv::kScratchBytes,
                  "attn_compressed_noalloc: %lld split partials need %lld bytes, more than the %lld-byte scratch",
                  (long long)partials, (long long)need, (long long)exkv::kScratchBytes);
     float* s = nullptr;
     const int rc = exkv::scratch_of_current_device(&s);
     if (rc != EXKV_OK) return rc;
-    float* ws_o = s;                                                // [B*Hq, nsplit, 128]
-    float* ws_m = ws_o + partials * 128;                            // [B*Hq, nsplit]
+    float* ws_o = s;                                                // [B*Hq, nsplit, D]
+    float* ws_m = ws_o + partials * D;                              // [B*Hq, nsplit]
     float* ws_l = ws_m + partials;
     // every partial is written by the split kernel before the merge reads it, so the
     // array's previous contents never matter; no arrival counters (merge as a second kernel)

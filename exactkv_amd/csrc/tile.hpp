@@ -1,5 +1,6 @@
 // Page loader and bit-exact rebuild shared by decode attention and decode_to_bf16.
 //
+// Head dim 128 (the tuned kernels); the templates at the end cover every head dim.
 // Lane layout (one wavefront of 64 lanes covers one 16-token page of one KV head):
 //   r = lane % 16   token within the page
 //   g = lane / 16   channel group: channels [16g, 16g+16) and [64+16g, 64+16g+16)
@@ -15,12 +16,12 @@
 namespace exkv {
 
 struct CSrc {                 // one compressed cache (reference cache.py:24-32)
-    const uint8_t* sm;        // [B, TS, H, 128]
-    const uint8_t* code;      // [B, TS, H, 64]
-    const uint8_t* base;      // [B, TS/16, H, 128]
+    const uint8_t* sm;        // [B, TS, H, D]
+    const uint8_t* code;      // [B, TS, H, D/2]
+    const uint8_t* base;      // [B, TS/16, H, D]
     const int32_t* rowmask;   // [B, TS/16, H]
     const int32_t* rowoff;    // [B, TS/16, H]
-    const uint16_t* raw;      // [raw_rows, 128] bf16
+    const uint16_t* raw;      // [raw_rows, D] bf16
     int64_t raw_rows;
 };
 
@@ -111,6 +112,109 @@ __device__ inline void load_bf16_row(const uint16_t* buf, int64_t row, int g, ui
     out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
     out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;
     out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
+}
+
+// ---------------------------------------------------------------- any head dim D
+//
+// The same lane layout for D = 64, 128 or 256: lane (r = token, g = lane / 16) holds the
+// channel runs [g R, g R + R) and [D/2 + g R, D/2 + g R + R), R = D / 8, whose codes share
+// the R code bytes g R .. (low and high nibbles). Values: D / 8 dwords of bf16 pairs, the
+// low run first; k-block kc of the score MFMAs takes dwords 4kc .. 4kc + 3.
+template <int D>
+struct Run {
+    static_assert(D == 64 || D == 128 || D == 256, "head dim 64, 128 or 256");
+    static constexpr int R = D / 8;        // channels per run
+    static constexpr int W = R / 4;        // dwords of bytes per run
+    static constexpr int V = D / 8;        // dwords of values per lane (two runs)
+};
+
+// n dwords from p (8- or 16-byte aligned for n = 2, n >= 4)
+template <int N>
+__device__ inline void ld_words(const void* p, uint32_t* out) {
+    if constexpr (N == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        out[0] = v.x; out[1] = v.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+            out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+        }
+    }
+}
+template <int N>
+__device__ inline void st_words(void* p, const uint32_t* in) {
+    if constexpr (N == 2) {
+        *reinterpret_cast<uint2*>(p) = make_uint2(in[0], in[1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i)
+            reinterpret_cast<uint4*>(p)[i] = make_uint4(in[4 * i], in[4 * i + 1], in[4 * i + 2], in[4 * i + 3]);
+    }
+}
+
+template <int D>
+struct PageBytesD {
+    uint32_t sm_lo[Run<D>::W], sm_hi[Run<D>::W], code[Run<D>::W], b_lo[Run<D>::W], b_hi[Run<D>::W];
+};
+
+// row: the lane's token row ((page * 16 + r) * H + h in the arrays); page: page * H + h.
+template <int D>
+__device__ inline void load_page_d(const CSrc& c, int64_t row, int64_t page, int g, PageBytesD<D>& pb) {
+    constexpr int R = Run<D>::R, W = Run<D>::W;
+    const uint8_t* s = c.sm + row * D + g * R;
+    ld_words<W>(s, pb.sm_lo);
+    ld_words<W>(s + D / 2, pb.sm_hi);
+    ld_words<W>(c.code + row * (D / 2) + g * R, pb.code);
+    const uint8_t* bp = c.base + page * D + g * R;
+    ld_words<W>(bp, pb.b_lo);
+    ld_words<W>(bp + D / 2, pb.b_hi);
+}
+
+template <int D, bool Z, bool HIGH>
+__device__ inline void rebuild_run_d(const uint32_t* sm, const uint32_t* code, const uint32_t* base, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < Run<D>::W; ++i) {
+        const uint32_t cn = (HIGH ? code[i] >> 4 : code[i]) & 0x0F0F0F0Fu;
+        rebuild4<Z>(sm[i], cn, base[i], out[2 * i], out[2 * i + 1]);
+    }
+}
+
+// The lane's D / 4 values; the zero-group fix-up per run, decided for the wavefront.
+template <int D>
+__device__ inline void rebuild_values_d(const PageBytesD<D>& pb, uint32_t (&out)[Run<D>::V]) {
+    constexpr int W = Run<D>::W;
+    uint32_t flo = 0, fhi = 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        flo |= pb.b_lo[i];
+        fhi |= pb.b_hi[i];
+    }
+    if (__ballot((flo & 0x80808080u) != 0) != 0)
+        rebuild_run_d<D, true, false>(pb.sm_lo, pb.code, pb.b_lo, out);
+    else
+        rebuild_run_d<D, false, false>(pb.sm_lo, pb.code, pb.b_lo, out);
+    if (__ballot((fhi & 0x80808080u) != 0) != 0)
+        rebuild_run_d<D, true, true>(pb.sm_hi, pb.code, pb.b_hi, out + 2 * W);
+    else
+        rebuild_run_d<D, false, true>(pb.sm_hi, pb.code, pb.b_hi, out + 2 * W);
+}
+
+// The lane's values of a bf16 row of D channels (a raw row, or a row of the bf16 twin).
+template <int D>
+__device__ inline void load_row_values_d(const uint16_t* rowp, int g, uint32_t (&out)[Run<D>::V]) {
+    constexpr int R = Run<D>::R;
+    ld_words<R / 2>(rowp + g * R, out);
+    ld_words<R / 2>(rowp + D / 2 + g * R, out + R / 2);
+}
+
+// Rebuild one page row of D channels, raw rows spliced in from the pool.
+template <int D>
+__device__ inline void rebuild_page_d(const CSrc& c, const PageBytesD<D>& pb, uint32_t rmask, int32_t roff, int r,
+                                      int g, uint32_t (&out)[Run<D>::V]) {
+    rebuild_values_d<D>(pb, out);
+    if (rmask != 0 && ((rmask >> r) & 1u))
+        load_row_values_d<D>(c.raw + raw_slot(rmask, roff, r, c.raw_rows) * D, g, out);
 }
 
 }  // namespace exkv

@@ -22,7 +22,7 @@ from . import _lib
 
 LOG2E = 1.4426950408889634
 P = 16
-D_SUPPORTED = 128
+HEAD_DIMS = (64, 128, 256)   # head dims the kernels are built for (128: the tuned attention kernels)
 
 
 def choose_split(B, Hkv, T, BLOCK_N, target=512):
@@ -49,12 +49,12 @@ _WS = {}  # split partials, reused per (device, stream, rows, nsplit): kernels o
 _CNT = {}  # merge arrival counters per (device, stream, units): zero between calls
 
 
-def _workspace(dev, rows, ns, st=None):
-    key = (dev.index, _lib.stream(dev.index) if st is None else st, rows, ns)
+def _workspace(dev, rows, ns, D, st=None):
+    key = (dev.index, _lib.stream(dev.index) if st is None else st, rows, ns, D)
     ws = _WS.get(key)
     if ws is None:
         f32 = dict(device=dev, dtype=torch.float32)
-        ws = _WS[key] = (torch.empty(rows, ns, D_SUPPORTED, **f32), torch.empty(rows, ns, **f32),
+        ws = _WS[key] = (torch.empty(rows, ns, D, **f32), torch.empty(rows, ns, **f32),
                          torch.empty(rows, ns, **f32))
     return ws
 
@@ -95,8 +95,8 @@ def _fused_counters(dev, B, Hkv, Hq, ns, fused_merge):
 
 
 def _check_q(q):
-    if q.dim() != 3 or q.shape[2] != D_SUPPORTED:
-        raise ValueError(f"q must be [B, Hq, 128] (got {tuple(q.shape)})")
+    if q.dim() != 3 or q.shape[2] not in HEAD_DIMS:
+        raise ValueError(f"q must be [B, Hq, D], D in {HEAD_DIMS} (got {tuple(q.shape)})")
     if q.dtype != torch.bfloat16 or not q.is_contiguous() or not q.is_cuda:
         raise ValueError("q must be a contiguous bf16 GPU tensor")
 
@@ -124,6 +124,11 @@ def _cache_args(c):
     if not isinstance(c, dict):
         c._abi_memo = (args, res)                      # kernel_args() is rebuilt when the pool grows
     return res
+
+
+def _cache_dim(c):
+    """Head dim of a CompressedKV or its buffers() dict (the sm array's last axis)."""
+    return (c["sm"] if isinstance(c, dict) else c.sm).shape[-1]
 
 
 def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window=0):
@@ -164,8 +169,8 @@ def _block_table_arg(block_table, B):
 
 def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
                          split_len=None, out=None, fused_merge=False, block_table=None, window=0):
-    """q [B, Hq, 128] bf16 contiguous; kc, vc: CompressedKV objects (or their .buffers()
-    dicts); T: valid tokens. Returns bf16 [B, Hq, 128], bit-identical to
+    """q [B, Hq, D] bf16 contiguous (D = 64, 128 or 256); kc, vc: CompressedKV objects (or
+    their .buffers() dicts) of head dim D; T: valid tokens. Returns bf16 [B, Hq, D], bit-identical to
     attention_reference on the same contents and split plan.
 
     block_table (int32 [B, max_pages], on the GPU): paged caches. kc / vc are then pools
@@ -180,6 +185,8 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     B, Hq, D = q.shape
     if (TSv, Hv) != (TS, Hkv) or (Bc < B or Bv < B if block_table is None else Bc != Bv):
         raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
+    if _cache_dim(kc) != D or _cache_dim(vc) != D:
+        raise ValueError(f"cache head dim {_cache_dim(kc)} / {_cache_dim(vc)} differs from q's {D}")
     if block_table is not None:
         bt, bts, cap = _block_table_arg(block_table, B)
         pool_pages = Bc * TS // P
@@ -188,7 +195,7 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
     st = _lib.stream(q.device.index)
-    wo, wm, wl = _workspace(q.device, B * Hq, ns, st)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns, D, st)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     if block_table is not None:
@@ -216,6 +223,8 @@ def attention_compressed_noalloc(q, kc, vc, T, *, out, lens=None, nsplit=None, s
     B, Hq, D = q.shape
     if (TSv, Hv) != (TS, Hkv) or Bc < B or Bv < B:
         raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
+    if _cache_dim(kc) != D or _cache_dim(vc) != D:
+        raise ValueError(f"cache head dim {_cache_dim(kc)} / {_cache_dim(vc)} differs from q's {D}")
     window = _window_arg(window)
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
@@ -226,11 +235,11 @@ def attention_compressed_noalloc(q, kc, vc, T, *, out, lens=None, nsplit=None, s
 
 def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, lens=None, nsplit=None,
                         split_len=None, out=None, fused_merge=False, block_table=None, window=0):
-    """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, 128] (contiguous);
+    """Same computation on uncompressed bf16 K, V of shape [B, TS, Hkv, D] (contiguous);
     with block_table, k and v are pools of pages as in attention_compressed."""
     _check_q(q)
     if k.shape != v.shape or k.dim() != 4 or k.dtype != torch.bfloat16 or not (k.is_contiguous() and v.is_contiguous()):
-        raise ValueError("k and v must be contiguous bf16 [B, TS, Hkv, 128] tensors of one shape")
+        raise ValueError("k and v must be contiguous bf16 [B, TS, Hkv, D] tensors of one shape")
     B, Hq, D = q.shape
     TS, Hkv = k.shape[1], k.shape[2]
     if (block_table is None and k.shape[0] < B) or k.shape[3] != D:
@@ -245,7 +254,7 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
     lp, lstride = _lens_arg(lens, B)
     st = _lib.stream(q.device.index)
-    wo, wm, wl = _workspace(q.device, B * Hq, ns, st)
+    wo, wm, wl = _workspace(q.device, B * Hq, ns, D, st)
     cnt = _fused_counters(q.device, B, Hkv, Hq, ns, fused_merge)
     out = torch.empty_like(q) if out is None else out
     if block_table is not None:
@@ -260,24 +269,25 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
 
 
 def decode_to_bf16(c, T, block_table=None):
-    """Compressed buffers (a buffers() dict or CompressedKV) -> bf16 [B, T, H, 128],
-    through the same page decoder attention uses. block_table (int32 [B, max_pages] on the
+    """Compressed buffers (a buffers() dict or CompressedKV) -> bf16 [B, T, H, D],
+    through the same page rebuild attention uses. block_table (int32 [B, max_pages] on the
     GPU): c is a pool of pages and sequence b's page p is pool page block_table[b, p]."""
     ka, TS, H, B = _cache_args(c)
+    D = _cache_dim(c)
     dev = (c["sm"] if isinstance(c, dict) else c.sm).device
     if block_table is not None:
         bt, bts, cap = _block_table_arg(block_table, block_table.shape[0])
         Bq = block_table.shape[0]
-        out = torch.empty(Bq, T, H, D_SUPPORTED, dtype=torch.bfloat16, device=dev)
-        _lib.call("exkv_decode_to_bf16_paged", *ka, B * TS // P, bt, bts, _lib.ptr(out), Bq, int(T), H,
-                  D_SUPPORTED, _lib.stream(dev.index))
+        out = torch.empty(Bq, T, H, D, dtype=torch.bfloat16, device=dev)
+        _lib.call("exkv_decode_to_bf16_paged", *ka, B * TS // P, bt, bts, _lib.ptr(out), Bq, int(T), H, D,
+                  _lib.stream(dev.index))
         return out
-    out = torch.empty(B, T, H, D_SUPPORTED, dtype=torch.bfloat16, device=dev)
-    _lib.call("exkv_decode_to_bf16", *ka, _lib.ptr(out), B, int(T), TS, H, D_SUPPORTED, _lib.stream())
+    out = torch.empty(B, T, H, D, dtype=torch.bfloat16, device=dev)
+    _lib.call("exkv_decode_to_bf16", *ka, _lib.ptr(out), B, int(T), TS, H, D, _lib.stream())
     return out
 
 
-def _check_source(src, strides, nb, npg, H):
+def _check_source(src, strides, nb, npg, H, D):
     if src.dtype != torch.bfloat16 or not src.is_cuda:
         raise ValueError("encode source must be a bf16 GPU tensor")
     if src.stride(-1) != 1:
@@ -285,7 +295,7 @@ def _check_source(src, strides, nb, npg, H):
     if any(s < 0 for s in strides):
         raise ValueError("negative source strides")
     s_b, s_pg, s_p, s_h = strides
-    last = (nb - 1) * s_b + (npg - 1) * s_pg + (P - 1) * s_p + (H - 1) * s_h + D_SUPPORTED - 1
+    last = (nb - 1) * s_b + (npg - 1) * s_pg + (P - 1) * s_p + (H - 1) * s_h + D - 1
     avail = src.untyped_storage().nbytes() // 2 - src.storage_offset()
     if nb > 0 and npg > 0 and last >= avail:
         raise ValueError(f"encode source too small: needs element {last}, has {avail}")
@@ -317,7 +327,7 @@ def encode_pages(src, strides, buf, b0, pg0, nb, npg, *, chained=True):
     slot scan (in a per-stream workspace); chained=False: the page kernel, then a
     three-launch scan (same bytes)."""
     H, TS, D = buf["H"], buf["TS"], buf["D"]
-    _check_source(src, strides, nb, npg, H)
+    _check_source(src, strides, nb, npg, H, D)
     raw = buf["raw"]
     before = buf.get("before")
     ws = _scan_ws(raw.device, int(nb) * int(npg) * H) if chained else None
@@ -334,7 +344,7 @@ def encode_pages_paged(src, strides, buf, dst_pages, nb, npg, *, chained=True):
     encode_pages) goes to page dst_pages[bi, pg] of the cache's arrays read as a list of
     B * TS / 16 pages. dst_pages: int32 [>= nb, >= npg] on the GPU."""
     H, TS, D = buf["H"], buf["TS"], buf["D"]
-    _check_source(src, strides, nb, npg, H)
+    _check_source(src, strides, nb, npg, H, D)
     if (dst_pages.dtype != torch.int32 or dst_pages.dim() != 2 or dst_pages.stride(1) != 1 or dst_pages.shape[0] < nb
             or dst_pages.shape[1] < npg):
         raise ValueError("dst_pages must be an int32 [nb, npg] tensor with unit column stride")
@@ -361,8 +371,8 @@ def _paged_append_args(x, table, slots):
 
 
 def append_paged(x, buf, table, slots=None):
-    """One token per row of x [n, H, 128] into a paged compressed cache (buf as for
-    encode_pages, arrays of a [1, 16 * pool_pages, H, 128] cache) whose slots, lengths and
+    """One token per row of x [n, H, D] into a paged compressed cache (buf as for
+    encode_pages, arrays of a [1, 16 * pool_pages, H, D] cache) whose slots, lengths and
     block table are those of `table` (lens already counting the new token)."""
     sp, lp, bp, bts, n, H, ms, mp = _paged_append_args(x, table, slots)
     raw = buf["raw"]
@@ -373,7 +383,7 @@ def append_paged(x, buf, table, slots=None):
 
 
 def append_paged_bf16(x, pool, table, slots=None):
-    """bf16 twin of append_paged over pool [1, 16 * pool_pages, H, 128]."""
+    """bf16 twin of append_paged over pool [1, 16 * pool_pages, H, D]."""
     sp, lp, bp, bts, n, H, ms, mp = _paged_append_args(x, table, slots)
     _lib.call("exkv_bf16_append_paged", _lib.ptr(x, align=2, what="x"), x.stride(0), x.stride(1), _lib.ptr(pool),
               sp, lp, bp, bts, n, H, ms, mp, pool.shape[0] * pool.shape[1] // P, x.shape[2], _lib.stream())

@@ -25,7 +25,7 @@ compact().
 import torch
 
 from . import _lib
-from .kernels import P, encode_pages_paged, append_paged, append_paged_bf16
+from .kernels import HEAD_DIMS, P, encode_pages_paged, append_paged, append_paged_bf16
 
 
 class PageTable:
@@ -162,7 +162,7 @@ class PagedCompressedKV:
     """One layer's keys (or values) for the pages of a PageTable, in the exactkv byte format."""
 
     def __init__(self, table, H, D=128, reserve=0.01):
-        assert D == 128, "D = 128 only (Qwen2/2.5/3, Llama-3 family)"
+        assert D in HEAD_DIMS, f"head dim must be one of {HEAD_DIMS} (got {D})"
         self.table, self.H, self.D = table, H, D
         dev = self.dev = table.dev
         NPg = table.num_pages

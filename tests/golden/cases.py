@@ -34,6 +34,22 @@ def _mixed_small():
     return x
 
 
+def _mixed_dim(D, seed):
+    # lognormal channel scales with one huge channel, signed zeros, a tiny row, inf and nan,
+    # at head dim D: channels on both sides of D/2 carry the specials
+    rng = np.random.Generator(np.random.PCG64(seed))
+    scale = np.array([math.exp(z) for z in rng.standard_normal(2 * D).tolist()], np.float32).reshape(2, D)
+    scale[1, D // 2 + 3] = 500.0
+    xf = rng.standard_normal((1, 48, 2, D), dtype=np.float32) * scale
+    x = torch.from_numpy(_bf16_bits(xf).astype(np.int16)).view(torch.bfloat16)
+    x[0, 3, 0, 1] = 0.0
+    x[0, 5, 1, D // 2] = -0.0
+    x[0, 20, 1, :] = 1e-30
+    x[0, 33, 0, D - 1] = float("inf")
+    x[0, 40, 1, D // 2 - 1] = float("nan")
+    return x
+
+
 CASES = {
     "allpat_identity": (lambda: all_bf16_patterns("identity"), True),
     "allpat_perm": (lambda: all_bf16_patterns("perm", seed=0), False),
@@ -44,4 +60,11 @@ CASES = {
     "mixed": (_mixed, False),
     "c0_keys": (lambda: make_kv(1, 4096, 4, kind="k", seed=0), False),
     "c0_values": (lambda: make_kv(1, 1024, 4, kind="v", seed=1), False),
+    # other head dims (the code byte pairs channel j with j + D/2)
+    "d64_stress": (lambda: stress_pages(2, 64, 3, D=64, seed=5), True),
+    "d256_stress": (lambda: stress_pages(1, 64, 2, D=256, seed=6), True),
+    "d64_mixed": (lambda: _mixed_dim(64, seed=9), True),
+    "d256_mixed": (lambda: _mixed_dim(256, seed=10), True),
+    "d64_keys": (lambda: make_kv(2, 1024, 2, D=64, kind="k", seed=7, raw_row_rate=0.01), False),
+    "d256_values": (lambda: make_kv(1, 512, 4, D=256, kind="v", seed=8, raw_row_rate=0.01), False),
 }

@@ -33,9 +33,15 @@ def test_library_exports_every_declared_symbol():
 
 def test_argument_errors_are_reported_without_launching():
     lib = _lib.load()
-    # head dim 64 is not a format size: rejected before any HIP call
-    rc = lib.exkv_decode_to_bf16(1, 1, 1, 1, 1, 1, 1, 1, 1, 16, 16, 1, 64, None)
+    # head dim 96 has no kernels (64, 128 and 256 do): rejected before any HIP call
+    rc = lib.exkv_decode_to_bf16(1, 1, 1, 1, 1, 1, 1, 1, 1, 16, 16, 1, 96, None)
     assert rc == 1 and b"head dim" in lib.exkv_last_error()
+    for fn, args in (("exkv_attn_reduce", (1, 1, 1, 1, 1, 1, 96, None)),
+                     ("exkv_bf16_append", (1, 0, 0, 1, 1, 1, 1, 16, 96, None))):
+        assert getattr(lib, fn)(*args) == 1 and b"head dim" in lib.exkv_last_error(), fn
+    # head dim 64 passes the head-dim check and fails on the next one (T past TS)
+    rc = lib.exkv_decode_to_bf16(1, 1, 1, 1, 1, 1, 1, 1, 1, 17, 16, 1, 64, None)
+    assert rc == 1 and b"outside" in lib.exkv_last_error()
     rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 5000, 4096, None, 0, 1, 4096, 0, 0.1, None)
     assert rc == 1 and b"outside" in lib.exkv_last_error()
     rc = lib.exkv_encode_pages(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 1, 0, 2, 1, 4, 64, 128, None, 0,

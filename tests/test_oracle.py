@@ -297,16 +297,16 @@ def test_tolerance_bound_rejects_plausible_mistakes():
 @pytest.mark.parametrize("name", [n for n, (_, stored) in cases.CASES.items() if stored])
 def test_bits_per_value_closed_form(golden, name):
     """bits_per_value (reference codec.py:76-78) on the reference-written buffers: with N raw
-    rows over B*T*H rows of 128 values it is 8 * (128 + 64 + 8 + 0.5 + 256 N / (B T H)) / 128
-    = 12.53125 + 16 N / (B T H): a page's 16 sm rows, 16 code rows, one base row and two
-    int32 per head, plus 256 bytes per raw row."""
+    rows over B*T*H rows of D values it is 8 * (D + D/2 + D/16 + 0.5 + 2 D N / (B T H)) / D
+    = 12.5 + 4 / D + 16 N / (B T H) (12.53125 + ... at D = 128): a page's 16 sm rows, 16
+    code rows, one base row and two int32 per head, plus 2 D bytes per raw row."""
     from exactkv_amd.codec import bits_per_value
     z, _ = golden
     c = {k: torch.from_numpy(np.ascontiguousarray(z[f"{name}/{k}"])) for k in FIELDS}
     B, T, H, D = c["sm"].shape
     N = c["raw"].shape[0]
-    assert D == 128
-    want = 12.53125 + 16.0 * N / (B * T * H)
+    assert D in (64, 128, 256)
+    want = 12.5 + 4.0 / D + 16.0 * N / (B * T * H)
     assert bits_per_value(c) == pytest.approx(want, rel=1e-12)
     if name in ("zeros", "constant"):
         assert N == 0 and bits_per_value(c) == 12.53125

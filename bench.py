@@ -61,11 +61,12 @@ def cpu_model():
     return platform.processor()
 
 
-def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0):
+def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0, D=128):
     """Bytes a decode-attention call must move: per K/V cache and valid token row
-    128 (sm) + 64 (code); per touched page and head 128 (base) + 8 (rowmask, rowoff);
-    256 per raw row referenced; plus q and the output. lens: per-sequence lengths;
-    window: only each sequence's last `window` tokens count."""
+    D (sm) + D/2 (code); per touched page and head D (base) + 8 (rowmask, rowoff);
+    2 D per raw row referenced; plus q and the output (head dim D: 192 + 136 per page +
+    256 per raw row at 128). lens: per-sequence lengths; window: only each sequence's last
+    `window` tokens count."""
     import torch
     lens = [T] * B if lens is None else [int(x) for x in lens]
     total = 0
@@ -78,8 +79,8 @@ def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0):
             tok = torch.arange(p0, npg, device=rm.device)[:, None] * 16 + bit   # [pages, 16]
             raw = (rm[:, :, None] >> bit) & 1                                 # [pages, Hkv, 16]
             raw_rows = int((raw * ((tok < L) & (tok >= lo))[:, None, :]).sum().item())
-            total += (L - lo) * Hkv * 192 + (npg - p0) * Hkv * 136 + raw_rows * 256
-    return total + 2 * B * Hq * 128 * 2
+            total += (L - lo) * Hkv * (3 * D // 2) + (npg - p0) * Hkv * (D + 8) + raw_rows * 2 * D
+    return total + 2 * B * Hq * D * 2
 
 
 def time_loop(fn, n, warmup, copies):
@@ -251,6 +252,9 @@ def main():
     ap.add_argument("--target-blocks", type=int, default=None)
     ap.add_argument("--window", type=int, default=0,
                     help="sliding-window attention over each sequence's last WINDOW tokens (0: all)")
+    ap.add_argument("--head-dim", type=int, default=128, choices=(64, 128, 256),
+                    help="head dim of the attention shapes (64 and 256 run the generic-head-dim kernels; "
+                         "the workload's heads and context stay)")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a 256 MiB copy kernel (for scaling FETCH_SIZE / WRITE_SIZE), "
                          "then a few launches of each attention kernel (with --workload c3: of the encoder "
@@ -281,13 +285,16 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
+    D = a.head_dim
+    if D != 128:
+        desc = f"{desc}, head dim {D}"
     print(f"[bench] {a.workload}: {desc}; generating data", file=sys.stderr, flush=True)
-    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=100, device=dev)
-    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=101, device=dev)
-    q = synthetic.make_q(B, Hq, seed=102, device=dev)
+    k = synthetic.make_kv(B, TS, Hkv, D=D, kind="k", seed=100, device=dev)
+    v = synthetic.make_kv(B, TS, Hkv, D=D, kind="v", seed=101, device=dev)
+    q = synthetic.make_q(B, Hq, D=D, seed=102, device=dev)
     kcs, vcs, kbs, vbs = [], [], [], []
     for i in range(a.copies):
-        kc, vc = exactkv.CompressedKV(B, TS, Hkv, 128), exactkv.CompressedKV(B, TS, Hkv, 128)
+        kc, vc = exactkv.CompressedKV(B, TS, Hkv, D), exactkv.CompressedKV(B, TS, Hkv, D)
         for b in range(B):
             kc.prefill_slot(b, k[b:b + 1, :T])
             vc.prefill_slot(b, v[b:b + 1, :T])
@@ -300,7 +307,10 @@ def main():
     print("[bench] caches encoded", file=sys.stderr, flush=True)
     W = a.window
     reach = min(T, W + 15) if W else T                 # the splits start at the window's first page
-    ns, sl = kernels.plan_splits(B, Hkv, Hq, reach, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
+    if a.target_blocks or D == 128:
+        ns, sl = kernels.plan_splits(B, Hkv, Hq, reach, **({"target_blocks": a.target_blocks} if a.target_blocks else {}))
+    else:
+        ns, sl = kernels.plan_splits_hd(B, Hkv, Hq, reach, D)
     out = torch.empty_like(q)
     if a.profile:
         profile_run(kernels, q, kcs[0], vcs[0], kbs[0], vbs[0], T, ns, sl, out)
@@ -325,23 +335,24 @@ def main():
     med, p10, p90 = time_calls(full_c, max(a.steps, 50), a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
 
-    alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv, window=W)
-    alg_b = 2 * B * min(T, W or T) * Hkv * 256 + 2 * B * Hq * 128 * 2
+    alg = algorithmic_bytes([kcs[0], vcs[0]], B, T, Hq, Hkv, window=W, D=D)
+    alg_b = 2 * B * min(T, W or T) * Hkv * 2 * D + 2 * B * Hq * D * 2
     gbps = alg / (ms_split * 1e-3) / 1e9
     enc = encoder_gbps(exactkv, kernels, kbs[:2], T, a.steps, a.warmup)
     print("[bench] encoder timed", file=sys.stderr, flush=True)
 
-    traffic, traffic_src = profiled_traffic(a.workload) if not W else (None, None)
+    traffic, traffic_src = profiled_traffic(a.workload) if not W and D == 128 else (None, None)
     res = {
         "metric": METRIC, "value": round(ms_c * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_c, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{a.workload}: {desc}", "B": B, "T": T, "TS": TS, "Hq": Hq, "Hkv": Hkv,
-                   "head_dim": 128, "page": 16, "nsplit": ns, "split_len": sl, "cache_copies": a.copies,
+                   "head_dim": D, "page": 16, "nsplit": ns, "split_len": sl, "cache_copies": a.copies,
                    "parallelism": "single GPU", **({"window": W} if W else {})},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel": "attn_split_kernel<compressed>", "algorithmic_bytes": alg,
+                     "kernel": "attn_split_kernel<compressed>" if D == 128 else f"attn_dgen_kernel<{D}, compressed>",
+                     "algorithmic_bytes": alg,
                      "kernel_us": round(ms_split * 1e3, 2), "kernel_us_median": round(ms_split_med * 1e3, 2),
                      "kernel_timing": "HIP events recorded at each split kernel's own start and end "
                                       "(hipExtLaunchKernelGGL) on its launch stream, back-to-back launches"},
@@ -355,11 +366,11 @@ def main():
         "bf16_split_GBps": round(alg_b / (ms_split_b * 1e-3) / 1e9, 1),
         "speedup_vs_bf16": round(ms_b / ms_c, 3),
         "bit_identical_to_bf16": bool(identical),
-        "bits_per_value": round((kcs[0].nbytes() + vcs[0].nbytes()) * 8 / (2 * B * TS * Hkv * 128), 3),
+        "bits_per_value": round((kcs[0].nbytes() + vcs[0].nbytes()) * 8 / (2 * B * TS * Hkv * D), 3),
         "encoder_GBps": enc,
         "gpu": torch.cuda.get_device_name(0),
     }
-    if not a.no_cpu_baseline and not W:                # the baseline is the full-context attention
+    if not a.no_cpu_baseline and not W and D == 128:   # the baseline is the full-context attention at the metric's shape
         res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, a.cpu_runs)
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
@@ -926,7 +937,7 @@ def split_only(kernels, q, kc, vc, T, ns, sl, compressed, lens=None, block_table
     """Launch only the split kernel (the dominant kernel) into the shared workspace."""
     from exactkv_amd import _lib
     B, Hq, D = q.shape
-    wo, wm, wl = kernels._workspace(q.device, B * Hq, ns)
+    wo, wm, wl = kernels._workspace(q.device, B * Hq, ns, D)
     scale = D ** -0.5 * kernels.LOG2E
     lp, lstride = (lens.data_ptr(), lens.stride(0)) if lens is not None else (None, 0)
     if block_table is not None:                        # compressed pool of pages
@@ -973,7 +984,7 @@ def encoder_gbps(exactkv, kernels, xs, T, steps, warmup):
     torch.cuda.synchronize()
     assert all(int(c.cnt.item()) <= c.cap for c in caches)
     rows = B * npg * 16 * H
-    byts = rows * 256 + rows * 192 + B * npg * H * 136 + sum(raw) / len(raw) * 256
+    byts = rows * 2 * D + rows * (3 * D // 2) + B * npg * H * (D + 8) + sum(raw) / len(raw) * 2 * D
     return round(byts / (ms * 1e-3) / 1e9, 1)
 
 

@@ -9,7 +9,7 @@ import os
 
 # EXACTKV_LIB overrides the path of the library to load (default: the in-tree build)
 _PATH = os.environ.get("EXACTKV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 
@@ -57,6 +57,7 @@ SIGNATURES = {
                                      _i32, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _f32, _p],
     "exkv_noalloc_scratch_bytes": [],
     "exkv_plan_splits": [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
+    "exkv_plan_splits_hd": [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],
     "exkv_last_error": [],
 }

@@ -8,11 +8,11 @@ from .kernels import attention_compressed, attention_reference
 def decode_attention(q, k_cache, v_cache, **kw):
     """Attention of one new query token per sequence over its cached keys and values.
 
-    q: bf16 [B, Hq, 128], contiguous, RoPE already applied. k_cache / v_cache: a matching
+    q: bf16 [B, Hq, D], contiguous, RoPE already applied (D = 64, 128 or 256). k_cache / v_cache: a matching
     pair -- CompressedKV, BF16KV, or PagedCompressedKV / PagedBF16KV of one PageTable (then
     row i of q belongs to the current step's slot i) -- whose appends for this step have
     already run, so the current token is attended to. Extra keywords go to the kernel call
-    (window=, nsplit=, split_len=, out=, ...). Returns bf16 [B, Hq, 128].
+    (window=, nsplit=, split_len=, out=, ...). Returns bf16 [B, Hq, D].
 
     A compressed pair and a bf16 pair holding the same tokens return the same bits for the
     same split plan. Any other cache type raises TypeError."""

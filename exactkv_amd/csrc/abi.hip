@@ -24,7 +24,7 @@ int hip_status(hipError_t e, const char* where) {
 
 }  // namespace exkv
 
-extern "C" int exkv_abi_version(void) { return 2; }
+extern "C" int exkv_abi_version(void) { return 3; }
 
 extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 
@@ -35,27 +35,15 @@ extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 // another at about one memory round trip each, so a few units are served best by many
 // short splits) and a split length that is a multiple of 32. Plays the role of the reference's choose_split
 // (kernels.py:273-277), which targets 512 programs for a 128-SM-class GPU.
-extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
-                                int32_t min_split, int32_t* nsplit, int32_t* split_len) {
-    EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits: bad arguments");
-    EXKV_REQUIRE(nsplit && split_len, "plan_splits: null output");
-    if (target_blocks <= 0) target_blocks = 256;
-    if (min_split <= 0) min_split = 64;
-    const int64_t hg = (Hq / Hkv + 15) / 16;
-    int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8)
-    while (m) {
-        const int t = hw % m;
-        hw = m;
-        m = t;
-    }
-    const int64_t units = (int64_t)B * (Hkv / hw) * hg;
-    // Up to target_blocks units: one round of about target_blocks workgroups (one per CU).
-    // More units than that: the fewest splits that give at least two rounds (the second
-    // round's workgroups start as the first ones end, which staggers the tail) with the
-    // last round at least 95% full (else the fullest within 16 splits). Every workgroup
-    // pays a first-page latency of a few us, so long splits win once the GPU is full:
-    // measured at B256 x 4352, 1/2/4/8 splits: 610/601/614/636 us; B620: 2 splits 1454 us,
-    // 4 splits 1490 us.
+// The split count for `units` workgroup units: up to target_blocks units, one round of
+// about target_blocks workgroups; more units than that: the fewest splits that give at
+// least two rounds (the second round's workgroups start as the first ones end, which
+// staggers the tail) with the last round at least 95% full (else the fullest within 16
+// splits). Every workgroup pays a first-page latency of a few us, so long splits win once
+// the GPU is full: measured at B256 x 4352, 1/2/4/8 splits: 610/601/614/636 us; B620: 2
+// splits 1454 us, 4 splits 1490 us.
+static void plan_core(int64_t units, int32_t T, int64_t target_blocks, int32_t min_split, int32_t* nsplit,
+                      int32_t* split_len) {
     int64_t ns = 1;
     if (units < target_blocks) {
         ns = (target_blocks + units - 1) / units;
@@ -79,5 +67,38 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
     sl = (sl + 31) / 32 * 32;
     *split_len = (int32_t)sl;
     *nsplit = (int32_t)(((int64_t)T + sl - 1) / sl);
+}
+
+extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
+                                int32_t min_split, int32_t* nsplit, int32_t* split_len) {
+    EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits: bad arguments");
+    EXKV_REQUIRE(nsplit && split_len, "plan_splits: null output");
+    if (target_blocks <= 0) target_blocks = 256;
+    if (min_split <= 0) min_split = 64;
+    const int64_t hg = (Hq / Hkv + 15) / 16;
+    int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8)
+    while (m) {
+        const int t = hw % m;
+        hw = m;
+        m = t;
+    }
+    plan_core((int64_t)B * (Hkv / hw) * hg, T, target_blocks, min_split, nsplit, split_len);
+    return EXKV_OK;
+}
+
+// Split plan of the head-dim 64 / 256 kernels: their workgroups cover one KV head and one
+// group of 16 query heads, and one round is every workgroup the GPU holds at once -- 4 per
+// CU at head dim 64 (4 wavefronts of <= 128 registers), 2 at 256 (2 wavefronts of ~360
+// registers) -- measured best at the c2a shape (B8 x 8192, 32q/8kv): 16 splits at 64 (36.6
+// against 37.9 us for 32), 8 at 256 (92.6 against 116.2 us for 32). Head dim 128: the plan
+// of exkv_plan_splits with its defaults.
+extern "C" int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t D, int32_t* nsplit,
+                                   int32_t* split_len) {
+    EXKV_REQUIRE(exkv::head_dim_ok(D), "plan_splits_hd: head dim must be 64, 128 or 256 (got %d)", D);
+    if (D == 128) return exkv_plan_splits(B, Hkv, Hq, T, 0, 0, nsplit, split_len);
+    EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits_hd: bad arguments");
+    EXKV_REQUIRE(nsplit && split_len, "plan_splits_hd: null output");
+    const int64_t units = (int64_t)B * Hkv * ((Hq / Hkv + 15) / 16);
+    plan_core(units, T, D == 64 ? 1024 : 512, 64, nsplit, split_len);
     return EXKV_OK;
 }

@@ -1308,7 +1308,11 @@ template <int D, bool COMP>
 __global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a) {
     using G = DGen<D>;
     constexpr int R = Run<D>::R;
-    constexpr bool kPrefetch = !(COMP && D >= 256);   // registers for a second page in flight
+    // page buffers per wavefront: while one page is worked on, the loads of the other
+    // kPD - 1 are in flight. Measured at the c2a shape: at D = 64 one buffer (more cost
+    // registers, 4 -> 2 wavefronts per SIMD: 37.9 / 40.9 / 45.2 us for 1 / 2 / 3); at 256
+    // two (three for the twin; 92.6 against 95.8 us)
+    constexpr int kPD = D == 64 ? 1 : (COMP ? 2 : 3);
     __shared__ __attribute__((aligned(16))) uint8_t lds[G::LDS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
     const int split = blockIdx.x;
@@ -1344,12 +1348,8 @@ __global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a
     const uint32_t tw = tile + (uint32_t)(r * G::TROW + 2 * g * R);                     // V tile row r, low run
     const uint32_t tr = tile + (uint32_t)((4 * g + (r >> 2)) * G::TROW + 8 * (r & 3));  // transpose reads
 
-    DPage<D, COMP> cur, nxt;
-    int p = p0 + wave;
-    if (p < pend) dgen_load<D, COMP>(a, b, NP, p, hk, r, g, cur);
-    for (; p < pend; p += G::NPH) {
-        const int pn = p + G::NPH;
-        if (kPrefetch && pn < pend) dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, nxt);
+    // one page: rebuild (or take) K and V, V into the tile, scores, softmax and P.V
+    auto page = [&](const DPage<D, COMP>& cur, int p) {
         uint32_t kd[G::V], vd[G::V];
         if constexpr (COMP) {
             rebuild_values_d<D>(cur.k, kd);
@@ -1390,10 +1390,22 @@ __global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a
         for (int nb = 0; nb < G::NB; ++nb)
             vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
         page_softmax_pv<G::NB>(sa, vt, ragged, t0, end, wlo, g, a.qk_scale, m_i, l_i, acc);
-        if constexpr (kPrefetch) {
-            cur = nxt;
-        } else if (pn < pend) {
-            dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, cur);
+    };
+    // pages p0 + wave + NPH j: buffer j % kPD holds page j, reloaded with page j + kPD as
+    // soon as page j is done
+    DPage<D, COMP> buf[kPD];
+    const int pfirst = p0 + wave;
+#pragma unroll
+    for (int i = 0; i < kPD; ++i)
+        if (pfirst + i * G::NPH < pend) dgen_load<D, COMP>(a, b, NP, pfirst + i * G::NPH, hk, r, g, buf[i]);
+    for (int p = pfirst; p < pend; p += kPD * G::NPH) {
+#pragma unroll
+        for (int i = 0; i < kPD; ++i) {
+            const int pi = p + i * G::NPH;
+            if (pi >= pend) break;
+            page(buf[i], pi);
+            const int pn = pi + kPD * G::NPH;
+            if (pn < pend) dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, buf[i]);
         }
     }
 
@@ -1453,12 +1465,16 @@ __global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a
 }
 
 // Split merge for head dims 64 and 256: one wavefront per (sequence, query head) row, lane
-// = D/64 consecutive channels, the splits summed in order with fmas (out = sum o_s w_s /
-// sum l_s w_s, w_s = 2^(m_s - max m)). Used by the compressed call and its twin alike.
+// = D/64 consecutive channels. The splits go in batches of 32 with every load of a batch in
+// flight (lane s of the batch reads m and l of split s, every lane its channels of each
+// split's o); the sums run over s in order with fmas (out = sum o_s w_s / sum l_s w_s, w_s
+// = 2^(m_s - max m)). Used by the compressed call and its twin alike.
 template <int D>
 __global__ void __launch_bounds__(64) attn_reduce_d_kernel(const float* po, const float* pm, const float* pl,
                                                            uint16_t* out, int ns) {
     constexpr int C = D / 64;
+    constexpr int NBATCH = 32;
+    typedef float fC __attribute__((ext_vector_type(C)));
     const int64_t row = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const float* m = pm + row * ns;
@@ -1467,20 +1483,33 @@ __global__ void __launch_bounds__(64) attn_reduce_d_kernel(const float* po, cons
     float M = -INFINITY;
     for (int s = lane; s < ns; s += 64) M = fmaxf(M, m[s]);
     M = wave_max(M);
-    float n[C], den = 0.f;
+    fC n;
 #pragma unroll
     for (int c = 0; c < C; ++c) n[c] = 0.f;
-    for (int s = 0; s < ns; ++s) {
-        const float w = fast_exp2(m[s] - M);
-        const float* os = o + (int64_t)s * D;
+    float den = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += NBATCH) {
+        const int nb = min(NBATCH, ns - s0);
+        const float mv = lane < nb ? m[s0 + lane] : -INFINITY;
+        const float lv = lane < nb ? l[s0 + lane] : 0.f;
+        fC v[NBATCH];
 #pragma unroll
-        for (int c = 0; c < C; ++c) n[c] = __builtin_fmaf(os[c], w, n[c]);
-        den = __builtin_fmaf(l[s], w, den);
+        for (int i = 0; i < NBATCH; ++i)
+            if (i < nb) v[i] = *reinterpret_cast<const fC*>(o + (int64_t)(s0 + i) * D);
+        const float ws = fast_exp2(mv - M);
+#pragma unroll
+        for (int i = 0; i < NBATCH; ++i)
+            if (i < nb) {
+                const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), i));
+                const float li = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), i));
+#pragma unroll
+                for (int c = 0; c < C; ++c) n[c] = __builtin_fmaf(v[i][c], w, n[c]);
+                den = __builtin_fmaf(li, w, den);
+            }
     }
     uint16_t* dst = out + row * D + lane * C;
     if constexpr (C == 1) {
-        const __bf16 v = (__bf16)(n[0] / den);
-        dst[0] = __builtin_bit_cast(uint16_t, v);
+        const __bf16 r = (__bf16)(n[0] / den);
+        dst[0] = __builtin_bit_cast(uint16_t, r);
     } else {
 #pragma unroll
         for (int c = 0; c < C; c += 2) reinterpret_cast<uint32_t*>(dst)[c / 2] = pack_bf16x2(n[c] / den, n[c + 1] / den);

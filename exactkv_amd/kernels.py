@@ -33,6 +33,14 @@ def choose_split(B, Hkv, T, BLOCK_N, target=512):
     return -(-T // split_len), split_len
 
 
+def plan_splits_hd(B, Hkv, Hq, T, D):
+    """Split plan for head dim D (exkv_plan_splits_hd): plan_splits' defaults at 128, one
+    round of the generic-head-dim kernel's workgroups at 64 and 256."""
+    ns, sl = ctypes.c_int32(), ctypes.c_int32()
+    _lib.call("exkv_plan_splits_hd", B, Hkv, Hq, T, D, ctypes.byref(ns), ctypes.byref(sl))
+    return ns.value, sl.value
+
+
 def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=64):
     """MI355X split plan (native): about `target_blocks` workgroups (one per CU) -- or about
     8x that many when there are more (sequence, head-block) units than workgroups in one
@@ -131,13 +139,13 @@ def _cache_dim(c):
     return (c["sm"] if isinstance(c, dict) else c.sm).shape[-1]
 
 
-def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window=0):
+def _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window=0, D=128):
     if nsplit is not None and split_len is not None:
         return nsplit, split_len
     reach = TS if lens is not None else T
     if window:                                 # the splits start at the window's first page
         reach = min(reach, window + P - 1)
-    return plan_splits(B, Hkv, Hq, reach)
+    return plan_splits(B, Hkv, Hq, reach) if D == 128 else plan_splits_hd(B, Hkv, Hq, reach, D)
 
 
 def _window_arg(window):
@@ -192,7 +200,7 @@ def attention_compressed(q, kc, vc, T, BLOCK_N=64, num_warps=4, num_stages=1, *,
         pool_pages = Bc * TS // P
         TS = cap
     window = _window_arg(window)
-    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window, D)
     lp, lstride = _lens_arg(lens, B)
     st = _lib.stream(q.device.index)
     wo, wm, wl = _workspace(q.device, B * Hq, ns, D, st)
@@ -226,7 +234,7 @@ def attention_compressed_noalloc(q, kc, vc, T, *, out, lens=None, nsplit=None, s
     if _cache_dim(kc) != D or _cache_dim(vc) != D:
         raise ValueError(f"cache head dim {_cache_dim(kc)} / {_cache_dim(vc)} differs from q's {D}")
     window = _window_arg(window)
-    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window, D)
     lp, lstride = _lens_arg(lens, B)
     _lib.call("exkv_attn_compressed_noalloc", _lib.ptr(q), *ka, *va, _lib.ptr(out), B, Hq, Hkv, D, int(T), TS, lp,
               lstride, ns, sl, window, D ** -0.5 * LOG2E, _lib.stream(q.device.index))
@@ -251,7 +259,7 @@ def attention_reference(q, k, v, T, BLOCK_N=64, num_warps=4, num_stages=1, *, le
         pool_pages = k.shape[0] * TS // P
         TS = cap
     window = _window_arg(window)
-    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window)
+    ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window, D)
     lp, lstride = _lens_arg(lens, B)
     st = _lib.stream(q.device.index)
     wo, wm, wl = _workspace(q.device, B * Hq, ns, D, st)

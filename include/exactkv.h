@@ -5,17 +5,19 @@
  * it stands in for is given above each declaration.
  *
  * Conventions
- *   - All pointers are device pointers (HIP), except the outputs of exkv_plan_splits.
+ *   - All pointers are device pointers (HIP), except the outputs of the split planners.
  *   - Work is enqueued on `stream` only; nothing synchronizes, nothing allocates, so
  *     calls can be captured in a HIP graph. The library holds no device state.
  *   - bf16 tensors are passed as raw 16-bit patterns. Tensors are row-major with the
  *     shapes given; "elements" strides count bf16 elements.
  *   - Return value: 0 ok, 1 invalid argument, 2 HIP launch error; exkv_last_error()
  *     returns the message of the last failure on the calling thread.
- *   - Head dim is 128 and pages hold 16 tokens (the only sizes the format defines).
+ *   - Pages hold 16 tokens. Head dim D is 64, 128 or 256 in every entry point that takes
+ *     one (the wire form: 128); the reference builds 128 only (cache.py:21), its codec
+ *     any D (code byte j holds channels j and j + D/2).
  *   - Compressed cache of one layer's keys or values (reference cache.py:24-32):
- *       sm [B, TS, H, 128] u8, code [B, TS, H, 64] u8, base [B, TS/16, H, 128] u8,
- *       rowmask, rowoff [B, TS/16, H] i32, raw [raw_rows, 128] bf16 with
+ *       sm [B, TS, H, D] u8, code [B, TS, H, D/2] u8, base [B, TS/16, H, D] u8,
+ *       rowmask, rowoff [B, TS/16, H] i32, raw [raw_rows, D] bf16 with
  *       raw_rows = cap + B*H*16 (rows that do not fit | open-page tail area),
  *       cnt / before: i32 pool counter and its value before the last encode.
  */
@@ -30,7 +32,8 @@ extern "C" {
 
 typedef struct ihipStream_t* hipStream_t;
 
-/* ABI version of the library (2: the encoders take a scan workspace). */
+/* ABI version of the library (2: the encoders take a scan workspace; 3: head dims 64 and
+ * 256 and exkv_plan_splits_hd). */
 int exkv_abi_version(void);
 
 /* Message of the last failed call on this thread. */
@@ -309,6 +312,13 @@ int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_
  * Replaces: kernels.py:273-277 choose_split. */
 int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);
+
+/* The split plan for head dim D (host pointers out): at 128 exkv_plan_splits with its
+ * defaults; at 64 and 256 one round of the generic-head-dim kernel's workgroups (one per
+ * KV head and group of 16 query heads; 1024 resident at 64, 512 at 256).
+ * No counterpart in the reference (head dim 128 only, cache.py:21). */
+int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t D, int32_t* nsplit,
+                        int32_t* split_len);
 
 #ifdef __cplusplus
 }

@@ -86,6 +86,24 @@ def test_plan_splits(B, Hkv, Hq, T, expect):
     assert sl % 32 == 0 and ns * sl >= T and (ns - 1) * sl < T
 
 
+@pytest.mark.parametrize("B,Hkv,Hq,T,D,expect", [
+    (8, 8, 32, 8192, 64, (16, 512)),     # 64 units (one per KV head) x 16 = 1024 resident workgroups
+    (8, 8, 32, 8192, 256, (8, 1024)),    # 64 units x 8 = 512 (two per CU)
+    (32, 2, 14, 4096, 64, (16, 256)),    # Qwen2.5-0.5B shape: 64 units
+    (1, 8, 32, 131072, 256, (64, 2048)),
+    (2, 2, 64, 1000, 64, (16, 64)),      # G = 32: two head groups per KV head, 8 units; capped by 64-token splits
+    (600, 8, 32, 4096, 64, (4, 1024)),   # 4800 units, 4.69 rounds: four splits fill the last round to 98.7%
+    (8, 8, 32, 8192, 128, (32, 256)),    # head dim 128: exkv_plan_splits
+])
+def test_plan_splits_hd(B, Hkv, Hq, T, D, expect):
+    from exactkv_amd.kernels import plan_splits, plan_splits_hd
+    ns, sl = plan_splits_hd(B, Hkv, Hq, T, D)
+    assert (ns, sl) == expect
+    assert sl % 32 == 0 and ns * sl >= T and (ns - 1) * sl < T
+    if D == 128:
+        assert (ns, sl) == plan_splits(B, Hkv, Hq, T)
+
+
 def test_rebuild_bitmath_exhaustive(tmp_path):
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):

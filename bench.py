@@ -244,6 +244,8 @@ def main():
     ap.add_argument("--e2e-prompt", type=int, default=4096)
     ap.add_argument("--e2e-gen", type=int, default=256)
     ap.add_argument("--e2e-batch", type=int, default=0, help="cap the e2e batch (0: as many as fit)")
+    ap.add_argument("--e2e-model", default="llama3.1-8b", choices=sorted(E2E_MODELS),
+                    help="the e2e model's shape (random init): c4's Llama-3.1-8B, or Llama-3.2-1B (head dim 64)")
     ap.add_argument("--e2e-work-gib", type=float, default=6.0,
                     help="memory kept free beyond the caches for activations, logits and pool growth")
     ap.add_argument("--copies", type=int, default=4, help="cache copies rotated to defeat the 256 MB MALL")
@@ -730,6 +732,11 @@ def cpu_sweep(a):
 E2E_CONFIG = dict(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                   num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
                   rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=False)
+# Llama-3.2-1B's shape: head dim 64 (2048 / 32), 8 KV heads, 16 layers, tied embeddings
+E2E_CONFIG_1B = dict(vocab_size=128256, hidden_size=2048, intermediate_size=8192, num_hidden_layers=16,
+                     num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
+                     rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=True)
+E2E_MODELS = {"llama3.1-8b": ("Llama-3.1-8B", E2E_CONFIG), "llama3.2-1b": ("Llama-3.2-1B (head dim 64)", E2E_CONFIG_1B)}
 
 
 def prefill_bench(a):
@@ -849,10 +856,11 @@ def e2e_paged(a):
 
 def e2e(a):
     """Config 4: batched greedy decoding with the engine on a random-init Llama-3.1-8B
-    (weights N(0, 0.02) bf16), prompts of uniform random token ids, the reference's
-    protocol (bench/e2e.py:43-101): KV budget = free memory after the weights minus
-    1.6 GiB, KV per sequence = kv_bytes(B=2) - kv_bytes(B=1), each backend at the largest
-    batch that fits, then the compressed cache also at the bf16 batch (same work)."""
+    (weights N(0, 0.02) bf16; --e2e-model llama3.2-1b: Llama-3.2-1B's shape, head dim 64),
+    prompts of uniform random token ids, the reference's protocol (bench/e2e.py:43-101): KV
+    budget = free memory after the weights minus 1.6 GiB, KV per sequence = kv_bytes(B=2) -
+    kv_bytes(B=1), each backend at the largest batch that fits, then the compressed cache
+    also at the bf16 batch (same work)."""
     import torch
     from transformers import LlamaConfig, LlamaForCausalLM
     import exactkv_amd as exactkv
@@ -861,10 +869,11 @@ def e2e(a):
     torch.cuda.set_device(dev)
     PL, G = a.e2e_prompt, a.e2e_gen
     TM = PL + G
-    print(f"[e2e] building random-init Llama-3.1-8B", file=sys.stderr, flush=True)
+    mname, mcfg = E2E_MODELS[a.e2e_model]
+    print(f"[e2e] building random-init {mname}", file=sys.stderr, flush=True)
     torch.manual_seed(0)
     with torch.device(dev):
-        model = LlamaForCausalLM(LlamaConfig(**E2E_CONFIG)).to(torch.bfloat16).eval()
+        model = LlamaForCausalLM(LlamaConfig(**mcfg)).to(torch.bfloat16).eval()
     torch.cuda.empty_cache()
     wbytes = sum(p.numel() * p.element_size() for p in model.parameters())
     budget = torch.cuda.mem_get_info()[0] - 1.6 * 2**30
@@ -883,7 +892,7 @@ def e2e(a):
     if a.e2e_batch:
         run_b = {be: min(a.e2e_batch, run_b[be]) for be in ps}
     g = torch.Generator().manual_seed(1)
-    ids = torch.randint(0, E2E_CONFIG["vocab_size"], (max(run_b.values()), PL), generator=g).to(dev)
+    ids = torch.randint(0, mcfg["vocab_size"], (max(run_b.values()), PL), generator=g).to(dev)
 
     def run(be, B):
         eng = exactkv.Engine(model, B, TM, backend=be)
@@ -918,10 +927,11 @@ def e2e(a):
     r_c, tok_c = run("exactkv", run_b["exactkv"])
     r_s, tok_s = run("exactkv", r_b["batch"])
     res = {
-        "metric": "e2e greedy decode tok/s (Llama-3.1-8B random init, 4096-token prompts, 256 new tokens)",
+        "metric": f"e2e greedy decode tok/s ({mname} random init, {PL}-token prompts, {G} new tokens)",
         "value": r_c["decode_tokens_per_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights N(0,0.02), random token ids)",
-        "config": {"workload": "c4: Llama-3.1-8B e2e greedy decode", "prompt": PL, "gen": G,
+        "config": {"workload": f"{'c4: ' if a.e2e_model == 'llama3.1-8b' else ''}{mname} e2e greedy decode",
+                   "prompt": PL, "gen": G, "head_dim": mcfg["hidden_size"] // mcfg["num_attention_heads"],
                    "weights_gib": round(wbytes / 2**30, 2), "kv_budget_gib": round(budget / 2**30, 2),
                    "sequences_fit": fit, "batch_run": run_b},
         "rows": [r_b, r_c, r_s],

@@ -1245,88 +1245,321 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
 // ---- split kernel for head dims 64 and 256 (the reference builds head dim 128 only,
 // cache.py:21; its kernels.py:142-194 at other head sizes)
 //
-// Grid: x = split, y = (sequence, KV head, group of 16 query heads). NPH wavefronts per
-// workgroup (page phases: 4 for D = 64, 2 for D = 256) take the split's pages round robin
+// Grid: one workgroup per (sequence, split, group of 16 query heads, KV head), numbered so
+// that the KV heads of one (sequence, split) run together on one XCD (see the kernel). NPH
+// wavefronts per workgroup (page phases: 4 for D = 64, 2 for D = 256) take the split's pages round robin
 // and are merged through LDS at the end, one partial per (split, query head), so the
-// workspace and the merge are those of the D = 128 kernels. Per page, each lane (token r,
-// channel group g) loads its share of the K and V bytes straight into VGPRs (the next
-// page's loads in flight behind the current page's work where registers allow), rebuilds
-// the values (tile.hpp, any head dim), splices raw rows from the pool, and runs the score
-// MFMAs, softmax and P.V of the D = 128 kernels: S^T = K Q^T with
-// v_mfma_f32_16x16x32_bf16 over D/32 k-blocks, V through a per-wavefront LDS tile (rows
-// of 2D + 32 bytes, so that the transposed reads touch every bank exactly twice) read as
-// the V^T operand with ds_read_b64_tr_b16 (lane (r, g) supplies row 4g + r/4, channels
-// 16nb + 4(r & 3) .. + 3, and receives channel 16nb + r of rows 4g .. 4g + 3). The bf16
-// twin is the same template over plain rows, so the two agree bit for bit.
-template <int D>
+// workspace and the merge are those of the D = 128 kernels.
+//
+// Memory pipeline: each wavefront brings its pages into its own NS-stage LDS ring with
+// direct-to-LDS loads (global_load_lds_dwordx4, 16 bytes per lane: one load per KiB of the
+// page's image), so that a page in flight costs no registers; a stage is read only after
+// the wavefront's own s_waitcnt vmcnt(n) for it (n = the loads issued after it). Row pieces
+// land XOR-swizzled (16-byte chunk c of row r at chunk c ^ key(r)), which keeps the later
+// reads of one chunk across 16 rows at the minimum of two LDS passes. A compressed page
+// with one or two raw rows (K and V together) brings them along with one more load into
+// the stage's raw slot; pages with more (rare) read them from the pool directly.
+//
+// Per page: lane (token r, channel group g) reads its bytes from the stage in the rebuild
+// layout (tile.hpp, any head dim), rebuilds K and V, splices raw rows, and runs the MFMA
+// formulation of the D = 128 kernels: S^T = K Q^T with v_mfma_f32_16x16x32_bf16 over D/32
+// k-blocks, and P.V from V^T read with ds_read_b64_tr_b16 (lane (r, g) supplies row
+// 4g + r/4, channels 16nb + 4(r & 3) .. + 3, and receives channel 16nb + r of rows 4g ..
+// 4g + 3) -- out of a per-wavefront tile of the rebuilt V (rows of 2D + 32 bytes, so each
+// bank serves two of a read's lanes), or, in the bf16 twin, straight out of its stage.
+// Both run the same arithmetic on the same values, so they agree bit for bit.
+template <int D, bool COMP>
 struct DGen {
     static constexpr int NPH = D >= 256 ? 2 : 4;     // page phases (wavefronts) per workgroup
+    static constexpr int R = Run<D>::R;             // channels per lane run
     static constexpr int V = Run<D>::V;             // value dwords per lane (K or V of a page)
     static constexpr int KC = D / 32;               // score MFMA k-blocks
     static constexpr int NB = D / 16;               // 16-channel blocks of V and O
-    static constexpr int TROW = 2 * D + 32;         // V tile row (bytes)
-    static constexpr int TILE = kPage * TROW;
-    static constexpr int MROW = D + 4;              // one head's partial in the merge (floats)
+    // page stage: compressed sm K [16][D] | sm V | code K [16][D/2] | code V | base K [D] |
+    // base V [D]; bf16 twin: K rows [16][2D] | V rows
+    static constexpr int SMK = 0, SMV = 16 * D, CODE = 32 * D, BASE = 48 * D;
+    static constexpr int BK = 0, BV = 32 * D;
+    static constexpr int STAGE = COMP ? 50 * D : 64 * D;
+    static constexpr int NDMA = COMP ? 3 * D / 64 + 1 : D / 16;   // 16-byte loads per lane and page
+    static constexpr int NS = COMP && D == 64 ? 3 : 2;             // ring stages per wavefront
+    static constexpr int NRAW = 2;                                // raw rows per page through the ring
+    static constexpr int RAWB = COMP ? NRAW * 2 * D : 0;          // a stage's raw slot
+    static constexpr int RING = NS * (STAGE + RAWB);
+    static constexpr int TROW = 2 * D + 32;                       // V tile row (bytes)
+    static constexpr int TILE = COMP ? kPage * TROW : 0;
+    static constexpr int PER_WAVE = RING + TILE;
+    static constexpr int LDS = NPH * PER_WAVE;
+    static constexpr int MROW = D + 4;                            // one head's partial in the merge (floats)
     static constexpr int MBYTES = (16 * MROW + 32) * 4;
-    static constexpr int LDS = NPH * TILE + (NPH - 1) * MBYTES;
+    static constexpr int MAXWAIT = (NS - 1) * (NDMA + 1);          // loads a stage's wait lets stay in flight
+    static_assert(RING >= MBYTES, "a wavefront's ring holds its partial for the merge");
+    static_assert(NDMA * 1024 >= STAGE && (NDMA - 1) * 1024 < STAGE, "one load per KiB of the stage");
+    static_assert(MAXWAIT <= 63, "the waits must fit vmcnt");
 };
 
-// One page as loaded by a lane: the K and V bytes (compressed) or values (bf16 twin).
+// Physical 16-byte chunk of logical chunk c in row r of an LDS image with rows of LB bytes:
+// c XOR the row's index among the rows that start on the same bank (rows LB apart cycle
+// through the 256 bytes of banks every 256 / LB rows).
+template <int LB>
+__device__ constexpr int dswz(int r, int c) {
+    constexpr int C = LB / 16, RPB = LB >= 256 ? 1 : 256 / LB;
+    return c ^ ((r / RPB) % C);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint2 lds8(const lds_u8* p) {
+    const u32x2 v = *reinterpret_cast<const EXKV_LDS u32x2*>(p);
+    return make_uint2(v.x, v.y);
+}
+
+// N bytes (8, 16, 32 or 64) of row r of a swizzled image at img, from logical byte b0
+// (8-aligned for N = 8, 16-aligned otherwise), as dwords.
+template <int LB, int N>
+__device__ inline void dread(uint32_t img, int r, int b0, uint32_t* out) {
+    if constexpr (N == 8) {
+        const uint2 v = lds8(lds_ptr(img + (uint32_t)(r * LB + dswz<LB>(r, b0 >> 4) * 16 + (b0 & 8))));
+        out[0] = v.x;
+        out[1] = v.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 16; ++i) {
+            const uint4 v = lds16(lds_ptr(img + (uint32_t)(r * LB + dswz<LB>(r, (b0 >> 4) + i) * 16)));
+            out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+        }
+    }
+}
+
+// A lane's loads of a page (fixed for the kernel): load i takes 16 bytes at off[i] from the
+// page's first row in its array (the K or the V array: bit i of vmask), lands them at stage
+// byte 1024 i + 16 lane, and is issued when bit i of act is set.
 template <int D, bool COMP>
-struct DPage;
-template <int D>
-struct DPage<D, true> {
-    PageBytesD<D> k, v;
+struct DLanes {
+    uint32_t off[DGen<D, COMP>::NDMA];
+    uint32_t vmask, act;
+};
+
+template <int D, bool COMP>
+__device__ inline DLanes<D, COMP> dgen_lanes(int Hkv, int lane) {
+    using G = DGen<D, COMP>;
+    DLanes<D, COMP> o{};
+#pragma unroll
+    for (int i = 0; i < G::NDMA; ++i) {
+        const int byte = 1024 * i + 16 * lane;         // in the stage image
+        bool v = false, on = true;
+        uint32_t off = 0;
+        if constexpr (COMP) {
+            if (byte < G::CODE) {                      // sm rows of D bytes
+                v = byte >= G::SMV;
+                const int b = byte - (v ? G::SMV : 0), row = b / D;
+                off = (uint32_t)(row * Hkv * D + dswz<D>(row, (b % D) >> 4) * 16);
+            } else if (byte < G::BASE) {               // code rows of D/2 bytes
+                v = byte >= G::CODE + 8 * D;
+                const int b = byte - G::CODE - (v ? 8 * D : 0), row = b / (D / 2);
+                off = (uint32_t)(row * Hkv * (D / 2) + dswz<D / 2>(row, (b % (D / 2)) >> 4) * 16);
+            } else {                                   // base rows of the page: K, then V
+                on = byte < G::STAGE;
+                v = byte >= G::BASE + D;
+                off = (uint32_t)((byte - G::BASE) % D);
+            }
+        } else {                                       // bf16 rows of 2D bytes
+            v = byte >= G::BV;
+            const int b = byte - (v ? G::BV : 0), row = b / (2 * D);
+            off = (uint32_t)(row * Hkv * 2 * D + dswz<2 * D>(row, (b % (2 * D)) >> 4) * 16);
+        }
+        o.off[i] = off;
+        o.vmask |= (v ? 1u : 0u) << i;
+        o.act |= (on ? 1u : 0u) << i;
+    }
+    return o;
+}
+
+struct DMeta {              // rowmask / rowoff of a page of the K and V caches (uniform)
     uint32_t mk, mv;
     int32_t ok, ov;
 };
-template <int D>
-struct DPage<D, false> {
-    uint32_t k[Run<D>::V], v[Run<D>::V];
-};
+__device__ inline bool draw_in_ring(const DMeta& m) {
+    const int n = __builtin_popcount(m.mk) + __builtin_popcount(m.mv);
+    return n > 0 && n <= 2;
+}
 
-template <int D, bool COMP>
-__device__ inline void dgen_load(const AttnArgs& a, int b, int NP, int p, int hk, int r, int g, DPage<D, COMP>& pg) {
-    const int64_t pidx = a.block_table == nullptr
-                             ? (int64_t)b * NP + p
-                             : (int64_t)min((uint32_t)a.block_table[b * a.bt_stride + p], (uint32_t)(a.pool_pages - 1));
-    const int64_t row = (pidx * kPage + r) * a.Hkv + hk, page = pidx * a.Hkv + hk;
+// Pool page of page p of sequence b (uniform): contiguous, or through the block table.
+__device__ inline int64_t dgen_pidx(const AttnArgs& a, int b, int NP, int p) {
+    if (a.block_table == nullptr) return (int64_t)b * NP + p;
+    return (int64_t)min((uint32_t)const_ld(a.block_table + b * a.bt_stride + p), (uint32_t)(a.pool_pages - 1));
+}
+
+template <bool COMP>
+__device__ inline DMeta dgen_meta(const AttnArgs& a, int64_t page) {
+    DMeta m{0u, 0u, 0, 0};
     if constexpr (COMP) {
-        load_page_d<D>(a.k, row, page, g, pg.k);
-        load_page_d<D>(a.v, row, page, g, pg.v);
-        pg.mk = (uint32_t)a.k.rowmask[page];
-        pg.mv = (uint32_t)a.v.rowmask[page];
-        pg.ok = a.k.rowoff[page];
-        pg.ov = a.v.rowoff[page];
+        m.mk = (uint32_t)const_ld(a.k.rowmask + page);
+        m.mv = (uint32_t)const_ld(a.v.rowmask + page);
+        m.ok = const_ld(a.k.rowoff + page);
+        m.ov = const_ld(a.v.rowoff + page);
+    }
+    return m;
+}
+
+// Issue a page's loads into stage st (and, compressed, its raw rows into raw_st when they
+// travel through the ring). Returns the number of loads issued.
+template <int D, bool COMP>
+__device__ inline int dgen_issue(const AttnArgs& a, const DLanes<D, COMP>& o, int64_t pidx, int hk, const DMeta& m,
+                                 uint32_t st, uint32_t raw_st, int lane) {
+    using G = DGen<D, COMP>;
+    const int64_t row0 = pidx * kPage * a.Hkv + hk, page = pidx * a.Hkv + hk;
+    // the stage (and its raw slot) was last read by this wavefront NS pages ago: those LDS
+    // reads complete before the loads can land there
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // the page's first row in each array, K and V (uniform; per-lane selects stay selects)
+    auto u64 = [](const void* p) { return (uint64_t)(uintptr_t)p; };
+    PairSrc sm{}, code{}, base{}, bf{};
+    if constexpr (COMP) {
+        sm = pair_src(u64(a.k.sm) + (uint64_t)row0 * D, u64(a.v.sm) + (uint64_t)row0 * D);
+        code = pair_src(u64(a.k.code) + (uint64_t)row0 * (D / 2), u64(a.v.code) + (uint64_t)row0 * (D / 2));
+        base = pair_src(u64(a.k.base) + (uint64_t)page * D, u64(a.v.base) + (uint64_t)page * D);
     } else {
-        load_row_values_d<D>(a.kb + row * D, g, pg.k);
-        load_row_values_d<D>(a.vb + row * D, g, pg.v);
+        bf = pair_src(u64(a.kb) + (uint64_t)row0 * (2 * D), u64(a.vb) + (uint64_t)row0 * (2 * D));
+    }
+#pragma unroll
+    for (int i = 0; i < G::NDMA; ++i) {
+        const bool v = (o.vmask >> i) & 1u;
+        const int byte = 1024 * i;                     // the load's array is fixed by its position
+        const PairSrc& ps = !COMP ? bf : (byte < G::CODE ? sm : (byte < G::BASE ? code : base));
+        if ((o.act >> i) & 1u) dma16((const void*)(uintptr_t)(ps.pick(v) + o.off[i]), st + 1024u * i);
+    }
+    int n = G::NDMA;
+    if constexpr (COMP) {
+        if (draw_in_ring(m)) {                         // uniform
+            // raw rows of the page (K rows in token order, then V rows): entry e = lane /
+            // (D/8), 16 bytes per lane; pool slot = rowoff + rank of the row
+            constexpr int LPR = D / 8;                 // lanes per raw row
+            const int nk = __builtin_popcount(m.mk), nr = nk + __builtin_popcount(m.mv), e = lane / LPR;
+            const bool isv = e >= nk;
+            int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
+            const int64_t rows = isv ? a.v.raw_rows : a.k.raw_rows;
+            idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+            const uint8_t* rb = reinterpret_cast<const uint8_t*>(isv ? a.v.raw : a.k.raw);
+            if (lane < LPR * nr) dma16(rb + idx * (2 * D) + (lane % LPR) * 16, raw_st);
+            ++n;
+        }
+    }
+    return n;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, N]
+template <int N>
+__device__ inline void dwait(int n) {
+    if constexpr (N > 0) {
+        if (n >= N) {
+            wait_vm<N>();
+            return;
+        }
+        dwait<N - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+// The lane's values of one raw row of the stage's raw slot (entry e: 2D bytes, unswizzled)
+template <int D>
+__device__ inline void draw_values(uint32_t raw_st, int e, int g, uint32_t (&out)[Run<D>::V]) {
+    constexpr int R = Run<D>::R;
+    const uint32_t p = raw_st + (uint32_t)(e * 2 * D + 2 * g * R);
+#pragma unroll
+    for (int i = 0; i < R / 8; ++i) {
+        const uint4 lo = lds16(lds_ptr(p) + 16 * i), hi = lds16(lds_ptr(p) + D + 16 * i);
+        out[4 * i] = lo.x; out[4 * i + 1] = lo.y; out[4 * i + 2] = lo.z; out[4 * i + 3] = lo.w;
+        out[R / 2 + 4 * i] = hi.x; out[R / 2 + 4 * i + 1] = hi.y; out[R / 2 + 4 * i + 2] = hi.z;
+        out[R / 2 + 4 * i + 3] = hi.w;
+    }
+}
+
+// K (V = false) or V of the stage's compressed page for lane (r, g): its bytes in the
+// rebuild layout, the rebuild, and its raw row spliced in (from the raw slot when the
+// page's raw rows came through the ring, else from the pool: rare, and it waits for every
+// load in flight).
+template <int D, bool V>
+__device__ inline void dgen_rebuild(const AttnArgs& a, uint32_t st, uint32_t raw_st, const DMeta& m, int r, int g,
+                                    uint32_t (&d)[Run<D>::V]) {
+    using G = DGen<D, true>;
+    constexpr int R = Run<D>::R;
+    PageBytesD<D> pb;
+    const uint32_t sm = st + (V ? G::SMV : G::SMK), code = st + G::CODE + (V ? 8 * D : 0);
+    dread<D, R>(sm, r, g * R, pb.sm_lo);
+    dread<D, R>(sm, r, D / 2 + g * R, pb.sm_hi);
+    dread<D / 2, R>(code, r, g * R, pb.code);
+    dread<D, R>(st + G::BASE + (V ? D : 0), 0, g * R, pb.b_lo);     // one row: no swizzle
+    dread<D, R>(st + G::BASE + (V ? D : 0), 0, D / 2 + g * R, pb.b_hi);
+    rebuild_values_d<D>(pb, d);
+    const uint32_t mask = V ? m.mv : m.mk;
+    if (mask != 0u) {                                  // uniform
+        keep_branch();
+        const bool take = ((mask >> r) & 1u) != 0;
+        uint32_t x[Run<D>::V];
+        if (draw_in_ring(m)) {
+            const int e = (V ? __builtin_popcount(m.mk) : 0) + __builtin_popcount(mask & ((1u << r) - 1u));
+            draw_values<D>(raw_st, min(e, G::NRAW - 1), g, x);
+        } else {
+            const CSrc& c = V ? a.v : a.k;
+            load_row_values_d<D>(c.raw + raw_slot(mask, V ? m.ov : m.ok, r, c.raw_rows) * D, g, x);
+            wait_vm<0>();
+            settle(x);
+        }
+#pragma unroll
+        for (int i = 0; i < Run<D>::V; ++i) d[i] = take ? x[i] : d[i];
     }
 }
 
 template <int D, bool COMP>
-__global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a) {
-    using G = DGen<D>;
-    constexpr int R = Run<D>::R;
-    // page buffers per wavefront: while one page is worked on, the loads of the other
-    // kPD - 1 are in flight. Measured at the c2a shape: at D = 64 one buffer (more cost
-    // registers, 4 -> 2 wavefronts per SIMD: 37.9 / 40.9 / 45.2 us for 1 / 2 / 3); at 256
-    // two (three for the twin; 92.6 against 95.8 us)
-    constexpr int kPD = D == 64 ? 1 : (COMP ? 2 : 3);
+__global__ void __launch_bounds__(64 * (D >= 256 ? 2 : 4)) attn_dgen_kernel(AttnArgs a) {
+    using G = DGen<D, COMP>;
+    static_assert(64 * G::NPH == 64 * (D >= 256 ? 2 : 4), "launch bounds");
+    constexpr int R = G::R, NS = G::NS;
     __shared__ __attribute__((aligned(16))) uint8_t lds[G::LDS];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
-    const int split = blockIdx.x;
-    int y = blockIdx.y;
-    const int hg = y % a.HG;
-    y /= a.HG;
-    const int hk = y % a.Hkv, b = y / a.Hkv;
-    int len = a.lens ? a.lens[b * a.lens_stride] : a.T;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // uniform, in an SGPR
+    // XCD-aware order: workgroups go to the 8 XCDs round robin (linear id mod 8), and a
+    // workgroup reads only its KV head's share of each token row (64 / 32-byte pieces at
+    // D = 64), so the KV heads of one (sequence, split) are given consecutive ids on one
+    // XCD, where they run together and share the L2 lines of their rows.
+    int item;
+    {
+        const int L = blockIdx.x, N = gridDim.x, q = N >> 3, rem = N & 7, x = L & 7, pos = L >> 3;
+        item = x < rem ? x * (q + 1) + pos : rem * (q + 1) + (x - rem) * q + pos;
+    }
+    const int hk = item % a.Hkv;
+    item /= a.Hkv;
+    const int hg = item % a.HG;
+    item /= a.HG;
+    const int split = item % a.nsplit, b = item / a.nsplit;
+    int len = a.lens ? const_ld(a.lens + b * a.lens_stride) : a.T;
     len = min(max(len, 0), a.TS);
     const int wlo = a.window > 0 ? max(len - a.window, 0) : 0;   // sliding window: tokens [wlo, len)
     const int start = (wlo & ~(kPage - 1)) + split * a.split_len;
     const int end = min(start + a.split_len, len);
     const int NP = a.TS / kPage, p0 = start / kPage, pend = end > start ? (end + kPage - 1) / kPage : p0;
     const int gh = min(16, a.G - hg * 16);
+
+    const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * G::PER_WAVE);   // this wavefront's (uniform)
+    auto stage = [&](int s) { return ring + (uint32_t)(s * G::STAGE); };
+    auto raw_slot_of = [&](int s) { return ring + (uint32_t)(NS * G::STAGE + s * G::RAWB); };
+    const DLanes<D, COMP> dl = dgen_lanes<D, COMP>(a.Hkv, lane);
+
+    // the first NS pages' loads leave before anything else
+    const int pfirst = p0 + wave;
+    DMeta meta[NS];
+    int cnt[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int p = pfirst + s * G::NPH;
+        cnt[s] = 0;
+        meta[s] = DMeta{0u, 0u, 0, 0};
+        if (p < pend) {
+            const int64_t pidx = dgen_pidx(a, b, NP, p);
+            meta[s] = dgen_meta<COMP>(a, pidx * a.Hkv + hk);
+            cnt[s] = dgen_issue<D, COMP>(a, dl, pidx, hk, meta[s], stage(s), raw_slot_of(s), lane);
+        }
+    }
 
     // Q^T operand: column = head hg*16 + r, k-block kc = channels of dwords 4kc.. of a lane's values
     bf16x8 qop[G::KC];
@@ -1338,84 +1571,104 @@ __global__ void __launch_bounds__(64 * DGen<D>::NPH) attn_dgen_kernel(AttnArgs a
             uint4 v = *reinterpret_cast<const uint4*>(qr + d0);
             if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
             qop[kc] = as_bf16x8(v.x, v.y, v.z, v.w);
+            asm volatile("" : "+v"(qop[kc]));
         }
     }
     f32x4 acc[G::NB];
 #pragma unroll
     for (int nb = 0; nb < G::NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_i = -INFINITY, l_i = 0.f;
-    const uint32_t tile = lds_addr(lds) + (uint32_t)(wave * G::TILE);
+    const uint32_t tile = ring + (uint32_t)G::RING;
     const uint32_t tw = tile + (uint32_t)(r * G::TROW + 2 * g * R);                     // V tile row r, low run
-    const uint32_t tr = tile + (uint32_t)((4 * g + (r >> 2)) * G::TROW + 8 * (r & 3));  // transpose reads
+    const uint32_t tr = tile + (uint32_t)((4 * g + (r >> 2)) * G::TROW + 8 * (r & 3));  // transposed reads
+    const int trow = 4 * g + (r >> 2);                 // twin: the row this lane's transposed reads supply
 
-    // one page: rebuild (or take) K and V, V into the tile, scores, softmax and P.V
-    auto page = [&](const DPage<D, COMP>& cur, int p) {
-        uint32_t kd[G::V], vd[G::V];
-        if constexpr (COMP) {
-            rebuild_values_d<D>(cur.k, kd);
-            if (cur.mk != 0u && ((cur.mk >> r) & 1u))
-                load_row_values_d<D>(a.k.raw + raw_slot(cur.mk, cur.ok, r, a.k.raw_rows) * D, g, kd);
-            rebuild_values_d<D>(cur.v, vd);
-            if (cur.mv != 0u && ((cur.mv >> r) & 1u))
-                load_row_values_d<D>(a.v.raw + raw_slot(cur.mv, cur.ov, r, a.v.raw_rows) * D, g, vd);
-        } else {
+    for (int p = pfirst; p < pend; p += NS * G::NPH) {
 #pragma unroll
-            for (int i = 0; i < G::V; ++i) {
-                kd[i] = cur.k[i];
-                vd[i] = cur.v[i];
-            }
-        }
-        const int t0 = p * kPage;
-        const bool ragged = t0 < wlo || t0 + kPage > end;
-        if (ragged) {                                  // rows outside [wlo, end) read as zero V
-            keep_branch();
-            if (t0 + r < wlo || t0 + r >= end) {
-#pragma unroll
-                for (int i = 0; i < G::V; ++i) vd[i] = 0u;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < R / 8; ++i) {              // the two runs of row r into the V tile
-            lds_st16(lds_ptr(tw) + 16 * i, vd[4 * i], vd[4 * i + 1], vd[4 * i + 2], vd[4 * i + 3]);
-            lds_st16(lds_ptr(tw) + D + 16 * i, vd[R / 2 + 4 * i], vd[R / 2 + 4 * i + 1], vd[R / 2 + 4 * i + 2],
-                     vd[R / 2 + 4 * i + 3]);
-        }
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < G::KC; ++kc)
-            sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]),
-                                                         qop[kc], sa, 0, 0, 0);
-        s16x4 vt[G::NB];
-#pragma unroll
-        for (int nb = 0; nb < G::NB; ++nb)
-            vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
-        page_softmax_pv<G::NB>(sa, vt, ragged, t0, end, wlo, g, a.qk_scale, m_i, l_i, acc);
-    };
-    // pages p0 + wave + NPH j: buffer j % kPD holds page j, reloaded with page j + kPD as
-    // soon as page j is done
-    DPage<D, COMP> buf[kPD];
-    const int pfirst = p0 + wave;
-#pragma unroll
-    for (int i = 0; i < kPD; ++i)
-        if (pfirst + i * G::NPH < pend) dgen_load<D, COMP>(a, b, NP, pfirst + i * G::NPH, hk, r, g, buf[i]);
-    for (int p = pfirst; p < pend; p += kPD * G::NPH) {
-#pragma unroll
-        for (int i = 0; i < kPD; ++i) {
-            const int pi = p + i * G::NPH;
+        for (int s = 0; s < NS; ++s) {
+            const int pi = p + s * G::NPH;
             if (pi >= pend) break;
-            page(buf[i], pi);
-            const int pn = pi + kPD * G::NPH;
-            if (pn < pend) dgen_load<D, COMP>(a, b, NP, pn, hk, r, g, buf[i]);
+            const int pn = pi + NS * G::NPH;
+            int64_t pidx_n = 0;
+            DMeta mn{0u, 0u, 0, 0};
+            if (pn < pend) {                           // the refill's metadata, early
+                pidx_n = dgen_pidx(a, b, NP, pn);
+                mn = dgen_meta<COMP>(a, pidx_n * a.Hkv + hk);
+            }
+            int after = 0;                             // loads issued after this stage's page
+#pragma unroll
+            for (int t = 0; t < NS; ++t)
+                if (t != s) after += cnt[t];
+            dwait<G::MAXWAIT>(after);
+            const uint32_t st = stage(s);
+            const int t0 = pi * kPage;
+            const bool ragged = t0 < wlo || t0 + kPage > end;
+            const bool valid = t0 + r >= wlo && t0 + r < end;
+            uint32_t kd[G::V];
+            s16x4 vt[G::NB];
+            if constexpr (COMP) {
+                uint32_t vd[G::V];
+                dgen_rebuild<D, true>(a, st, raw_slot_of(s), meta[s], r, g, vd);
+                if (ragged && !valid) {                // rows outside [wlo, end) read as zero V
+#pragma unroll
+                    for (int i = 0; i < G::V; ++i) vd[i] = 0u;
+                }
+#pragma unroll
+                for (int i = 0; i < R / 8; ++i) {      // the two runs of row r into the V tile
+                    lds_st16(lds_ptr(tw) + 16 * i, vd[4 * i], vd[4 * i + 1], vd[4 * i + 2], vd[4 * i + 3]);
+                    lds_st16(lds_ptr(tw) + D + 16 * i, vd[R / 2 + 4 * i], vd[R / 2 + 4 * i + 1],
+                             vd[R / 2 + 4 * i + 2], vd[R / 2 + 4 * i + 3]);
+                }
+                dgen_rebuild<D, false>(a, st, raw_slot_of(s), meta[s], r, g, kd);
+#pragma unroll
+                for (int nb = 0; nb < G::NB; ++nb)
+                    vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
+            } else {
+                dread<2 * D, 2 * R>(st + G::BK, r, 2 * g * R, kd);
+                dread<2 * D, 2 * R>(st + G::BK, r, D + 2 * g * R, kd + R / 2);
+                const uint32_t vs = st + G::BV;
+                if (ragged) {                          // rows outside [wlo, end) read as zero V
+                    keep_branch();
+                    if (!valid) {
+#pragma unroll
+                        for (int i = 0; i < 2 * R / 16; ++i) {
+                            lds_st16(lds_ptr(vs + (uint32_t)(r * 2 * D + dswz<2 * D>(r, (2 * g * R >> 4) + i) * 16)),
+                                     0u, 0u, 0u, 0u);
+                            lds_st16(lds_ptr(vs + (uint32_t)(r * 2 * D + dswz<2 * D>(r, ((D + 2 * g * R) >> 4) + i) * 16)),
+                                     0u, 0u, 0u, 0u);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int nb = 0; nb < G::NB; ++nb) {
+                    const int c = 2 * nb + ((r & 3) >> 1);    // logical chunk of channels 16nb + 4(r & 3) ..
+                    const uint32_t ad = vs + (uint32_t)(trow * 2 * D + dswz<2 * D>(trow, c) * 16 + 8 * (r & 1));
+                    vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(ad));
+                }
+            }
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < G::KC; ++kc)
+                sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(kd[4 * kc], kd[4 * kc + 1], kd[4 * kc + 2], kd[4 * kc + 3]), qop[kc], sa, 0, 0, 0);
+            page_softmax_pv<G::NB>(sa, vt, ragged, t0, end, wlo, g, a.qk_scale, m_i, l_i, acc);
+            // refill the stage with page pn
+            cnt[s] = 0;
+            if (pn < pend) {
+                meta[s] = mn;
+                cnt[s] = dgen_issue<D, COMP>(a, dl, pidx_n, hk, mn, st, raw_slot_of(s), lane);
+            }
         }
     }
 
     // page phases -> one partial per (split, query head): phase w > 0 leaves (o, m, l) in
-    // the merge area, phase 0 merges them in order (M = max m, o = sum o 2^(m - M), l alike)
+    // its own ring (no loads are in flight: every issued page was consumed), phase 0
+    // merges them in order (M = max m, o = sum o 2^(m - M), l alike)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     const float l_t = group_sum(l_i);
-    const uint32_t mb = lds_addr(lds) + (uint32_t)(G::NPH * G::TILE);
-    auto mo = [&](int w) { return mb + (uint32_t)((w - 1) * G::MBYTES); };
+    auto mo = [&](int w) { return lds_addr(lds) + (uint32_t)(w * G::PER_WAVE); };
     if (wave > 0) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int nb = 0; nb < G::NB; ++nb)
             *reinterpret_cast<EXKV_LDS f32x4*>(lds_ptr(mo(wave) + 4u * (r * G::MROW + 16 * nb + 4 * g))) = acc[nb];
@@ -1552,6 +1805,8 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
     }
     EXKV_REQUIRE((int64_t)B * (D == kD ? Hkv / heads_per_block(Hkv) : Hkv) * ((Hq / Hkv + 15) / 16) < 65536,
                  "attention: too many (sequence, head block) units");
+    EXKV_REQUIRE(D == kD || (int64_t)nsplit * B * Hkv * ((Hq / Hkv + 15) / 16) <= INT32_MAX,
+                 "attention: too many workgroups (%d splits)", nsplit);
     return EXKV_OK;
 }
 
@@ -1561,7 +1816,8 @@ static thread_local hipEvent_t t_split_start = nullptr, t_split_stop = nullptr;
 
 template <int D>
 static void launch_dgen(bool comp, const AttnArgs& a, hipEvent_t e0, hipEvent_t e1, hipStream_t stream) {
-    const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * a.Hkv * a.HG)), block(64 * DGen<D>::NPH);
+    // one-dimensional: the kernel orders (sequence, split, head group, KV head) itself
+    const dim3 grid((unsigned)((int64_t)a.nsplit * a.B * a.Hkv * a.HG)), block(64 * DGen<D, true>::NPH);
     auto k = comp ? attn_dgen_kernel<D, true> : attn_dgen_kernel<D, false>;
     if (e0 || e1)
         hipExtLaunchKernelGGL(k, grid, block, 0, stream, e0, e1, 0, a);

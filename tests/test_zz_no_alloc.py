@@ -15,19 +15,21 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _case(B, T, Hq, Hkv, seed):
+def _case(B, T, Hq, Hkv, seed, D=128):
     TS = -(-T // 16) * 16
-    k = synthetic.make_kv(B, TS, Hkv, kind="k", seed=seed, raw_row_rate=0.01).to(DEV)
-    v = synthetic.make_kv(B, TS, Hkv, kind="v", seed=seed + 1, raw_row_rate=0.01).to(DEV)
-    q = synthetic.make_q(B, Hq, seed=seed + 2).to(DEV)
+    k = synthetic.make_kv(B, TS, Hkv, D=D, kind="k", seed=seed, raw_row_rate=0.01).to(DEV)
+    v = synthetic.make_kv(B, TS, Hkv, D=D, kind="v", seed=seed + 1, raw_row_rate=0.01).to(DEV)
+    q = synthetic.make_q(B, Hq, D=D, seed=seed + 2).to(DEV)
     return q, _encode(k), _encode(v)
 
 
-@pytest.mark.parametrize("B,T,Hq,Hkv,ns", [(8, 8192, 32, 8, None), (3, 1000, 28, 4, 7)])
-def test_noalloc_equals_the_workspace_call(B, T, Hq, Hkv, ns):
-    print("[case] noalloc", B, T, Hq, Hkv, ns, flush=True)
-    big = _case(B, T, Hq, Hkv, seed=301)
-    small = _case(max(1, B // 2), T // 3 + 5, Hq, Hkv, seed=311)
+# head dims 64 and 256: the partials take (D + 2) floats each in the same scratch
+@pytest.mark.parametrize("B,T,Hq,Hkv,ns,D", [(8, 8192, 32, 8, None, 128), (3, 1000, 28, 4, 7, 128),
+                                             (4, 2000, 14, 2, None, 64), (2, 1500, 16, 4, 5, 256)])
+def test_noalloc_equals_the_workspace_call(B, T, Hq, Hkv, ns, D):
+    print("[case] noalloc", B, T, Hq, Hkv, ns, D, flush=True)
+    big = _case(B, T, Hq, Hkv, seed=301, D=D)
+    small = _case(max(1, B // 2), T // 3 + 5, Hq, Hkv, seed=311, D=D)
     for q, kc, vc in (big, small):                  # two calls in a row, the second smaller
         Tq = kc.TS if kc.TS < T else T
         nsplit = sl = None

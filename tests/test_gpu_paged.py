@@ -160,17 +160,20 @@ def _gather(pool_bf16, pages, T):
     return pool_bf16[0][rows.to(pool_bf16.device)]
 
 
-def test_paged_cache_prefill_append_release_compact():
+@pytest.mark.parametrize("D", [128, 64, 256])
+def test_paged_cache_prefill_append_release_compact(D):
     """A PageTable shared by paged K/V caches and their bf16 twins: prefills of ragged
     lengths, decode steps over dense and permuted slot subsets, a forced raw-pool overflow,
     release + reuse of pages and compact(). After every step the compressed and bf16 paged
-    attention agree bit for bit; the decoded pool equals the tokens written."""
-    H, Hq, D = 4, 16, 128
+    attention agree bit for bit; the decoded pool equals the tokens written. At head dims
+    128, 64 and 256 (the paged encoder and appends are templates on the head dim)."""
+    H, Hq = 4, 16
     table = exactkv.PageTable(num_pages=64, max_seqs=4, max_pages=16)
-    kc, vc = exactkv.PagedCompressedKV(table, H, reserve=1e-4), exactkv.PagedCompressedKV(table, H, reserve=1e-4)
-    kb, vb = exactkv.PagedBF16KV(table, H), exactkv.PagedBF16KV(table, H)
-    src_k = synthetic.make_kv(6, 256, H, kind="k", seed=81, raw_row_rate=0.05)
-    src_v = synthetic.make_kv(6, 256, H, kind="v", seed=82, raw_row_rate=0.05)
+    kc, vc = (exactkv.PagedCompressedKV(table, H, D=D, reserve=1e-4),
+              exactkv.PagedCompressedKV(table, H, D=D, reserve=1e-4))
+    kb, vb = exactkv.PagedBF16KV(table, H, D=D), exactkv.PagedBF16KV(table, H, D=D)
+    src_k = synthetic.make_kv(6, 256, H, D=D, kind="k", seed=81, raw_row_rate=0.05)
+    src_v = synthetic.make_kv(6, 256, H, D=D, kind="v", seed=82, raw_row_rate=0.05)
     truth = {}                                          # slot -> (k rows, v rows) on the CPU
 
     def prefill(seq, T):
@@ -192,7 +195,7 @@ def test_paged_cache_prefill_append_release_compact():
         for c, x in ((kc, xk), (vc, xv), (kb, xk), (vb, xv)):
             c.append(x.to(DEV).contiguous())
         if check:
-            q = synthetic.make_q(len(rows), Hq, seed=table.step).to(DEV)
+            q = synthetic.make_q(len(rows), Hq, D=D, seed=table.step).to(DEV)
             o_c = exactkv.decode_attention(q, kc, vc)
             o_b = exactkv.decode_attention(q, kb, vb)
             assert same_bits(o_c, o_b), f"step {table.step}"
@@ -258,8 +261,8 @@ def test_paged_cache_prefill_append_release_compact():
     for i, s in enumerate(rows):
         kk[i, :lens[i]] = torch.stack(truth[s][0])
         vv[i, :lens[i]] = torch.stack(truth[s][1])
-    q = synthetic.make_q(len(rows), Hq, seed=table.step)
-    _say("paged cache: oracle", lens)
+    q = synthetic.make_q(len(rows), Hq, D=D, seed=table.step)
+    _say("paged cache: oracle", D, lens)
     o_c = exactkv.decode_attention(q.to(DEV), kc, vc)
     assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(kk), u16(vv), Tm, np.float32, lens=lens))
 

@@ -34,6 +34,8 @@ WORKLOADS = {   # name: (B, T, TS, Hq, Hkv, description)
     "c2a_ragged": (8, 8185, 8192, 32, 8, "Llama-3.1-8B decode attention 32q/8kv, B8 x 8185 ctx (partial page)"),
     "c2b": (1, 131072, 131072, 32, 8, "Llama-3.1-8B decode attention 32q/8kv, B1 x 131072 ctx"),
     "c1": (1, 32768, 32768, 28, 4, "Qwen2.5-7B decode attention 28q/4kv, B1 x 32768 ctx"),
+    # a serving batch: long splits (one per sequence at head dims 64 / 256)
+    "long": (128, 4352, 4352, 32, 8, "decode attention 32q/8kv, B128 x 4352 ctx (serving batch)"),
 }
 
 

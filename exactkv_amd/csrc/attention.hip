@@ -1246,10 +1246,10 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
 // cache.py:21; its kernels.py:142-194 at other head sizes)
 //
 // Grid: one workgroup per (sequence, split, group of 16 query heads, KV head), numbered so
-// that the KV heads of one (sequence, split) run together on one XCD (see the kernel). NPH
-// wavefronts per workgroup (page phases: 4 for D = 64, 2 for D = 256) take the split's pages round robin
-// and are merged through LDS at the end, one partial per (split, query head), so the
-// workspace and the merge are those of the D = 128 kernels.
+// that the KV heads of one (sequence, split) run together on one XCD (see the kernel).
+// NPH wavefronts per workgroup (page phases: 4 for D = 64, 2 for D = 256) take the
+// split's pages round robin and are merged through LDS at the end, one partial per
+// (split, query head), so the workspace and the merge are those of the D = 128 kernels.
 //
 // Memory pipeline: each wavefront brings its pages into its own NS-stage LDS ring with
 // direct-to-LDS loads (global_load_lds_dwordx4, 16 bytes per lane: one load per KiB of the

@@ -17,7 +17,8 @@
 //                          the counter.
 // The append path (cache.py:100-112) runs a write (+ page encode), a one-workgroup slot
 // scan and a raw-row copy with the token count read from device memory, so a decode step
-// can be captured in a HIP graph.
+// can be captured in a HIP graph. Every kernel that touches rows is a template on the
+// head dim (64, 128 or 256); the entry points pick the instance.
 #include "tile.hpp"
 #include "../../include/exactkv.h"
 

@@ -292,6 +292,8 @@ def main():
     D = a.head_dim
     if D != 128:
         desc = f"{desc}, head dim {D}"
+    # the c4 protocol's sequences-fit on this GPU, before the workload's data takes memory
+    fit = e2e_fit() if a.workload == "c2a" and D == 128 and not a.window and not a.profile else None
     print(f"[bench] {a.workload}: {desc}; generating data", file=sys.stderr, flush=True)
     k = synthetic.make_kv(B, TS, Hkv, D=D, kind="k", seed=100, device=dev)
     v = synthetic.make_kv(B, TS, Hkv, D=D, kind="v", seed=101, device=dev)
@@ -377,6 +379,8 @@ def main():
     if not a.no_cpu_baseline and not W and D == 128:   # the baseline is the full-context attention at the metric's shape
         res["cpu_baseline"] = cpu_baseline(kcs[0], vcs[0], q, B, T, a.cpu_runs)
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
+    if fit is not None:
+        res["e2e_fit"] = fit
     print(json.dumps(res), flush=True)
 
 
@@ -739,6 +743,48 @@ E2E_CONFIG_1B = dict(vocab_size=128256, hidden_size=2048, intermediate_size=8192
                      num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=131072, rope_theta=5e5,
                      rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=True)
 E2E_MODELS = {"llama3.1-8b": ("Llama-3.1-8B", E2E_CONFIG), "llama3.2-1b": ("Llama-3.2-1B (head dim 64)", E2E_CONFIG_1B)}
+
+
+def e2e_fit(model_key="llama3.1-8b", prompt=4096, gen=256):
+    """The sequences-fit half of the c4 protocol (reference bench/e2e.py:54-63), measured
+    without running the model: a placeholder of the model's weight bytes (the parameter
+    shapes of its config, built on the meta device) is allocated, the KV budget is the free
+    device memory after it minus 1.6 GiB, and the KV per sequence is kv_bytes(B=2) -
+    kv_bytes(B=1) of every layer's K and V cache at T_max = prompt + gen, as the engine
+    builds them. Decode tok/s needs the prefill of every sequence: `--workload e2e`."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import exactkv_amd as exactkv
+
+    mname, cfg = E2E_MODELS[model_key]
+    with torch.device("meta"):
+        m = LlamaForCausalLM(LlamaConfig(**cfg))
+    wbytes = sum(p.numel() for p in m.parameters()) * 2          # bf16; tied weights counted once
+    del m
+    dev = torch.device("cuda", 0)
+    torch.cuda.empty_cache()
+    w = torch.empty(wbytes, dtype=torch.uint8, device=dev)
+    budget = torch.cuda.mem_get_info()[0] - 1.6 * 2**30
+    L, Hkv = cfg["num_hidden_layers"], cfg["num_key_value_heads"]
+    D = cfg["hidden_size"] // cfg["num_attention_heads"]
+    TS = -(-(prompt + gen) // 16) * 16
+
+    def kv_bytes(cls, B):
+        c = cls(B, TS, Hkv, D, device=dev)
+        n = c.nbytes()
+        del c
+        return 2 * L * n                                           # every layer's K and V cache
+
+    per_seq = {be: kv_bytes(cls, 2) - kv_bytes(cls, 1)
+               for be, cls in (("bf16", exactkv.BF16KV), ("exactkv", exactkv.CompressedKV))}
+    del w
+    torch.cuda.empty_cache()
+    fit = {be: int(budget // n) for be, n in per_seq.items()}
+    return {"model": f"{mname} (weights as a placeholder allocation)", "t_max": prompt + gen,
+            "weights_gib": round(wbytes / 2**30, 2), "kv_budget_gib": round(budget / 2**30, 2),
+            "kv_mib_per_seq": {be: round(n / 2**20, 1) for be, n in per_seq.items()},
+            "sequences_fit": fit, "ratio": round(fit["exactkv"] / fit["bf16"], 3),
+            "tok_s": "bench.py --workload e2e (the prefill of every sequence; minutes)"}
 
 
 def prefill_bench(a):

@@ -1805,8 +1805,12 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
     }
     EXKV_REQUIRE((int64_t)B * (D == kD ? Hkv / heads_per_block(Hkv) : Hkv) * ((Hq / Hkv + 15) / 16) < 65536,
                  "attention: too many (sequence, head block) units");
-    EXKV_REQUIRE(D == kD || (int64_t)nsplit * B * Hkv * ((Hq / Hkv + 15) / 16) <= INT32_MAX,
-                 "attention: too many workgroups (%d splits)", nsplit);
+    // a launch's grid is 32-bit in work-items: x = splits (head dim 128; the compressed
+    // kernel's workgroups are the larger) or every workgroup (the one-dimensional grid of
+    // the other head dims, DGen<D, *>::NPH wavefronts each)
+    const int64_t wg_x = D == kD ? (int64_t)nsplit : (int64_t)nsplit * B * Hkv * ((Hq / Hkv + 15) / 16);
+    const int64_t wg_threads = D == kD ? kCompThreads : 64 * (D >= 256 ? 2 : 4);
+    EXKV_REQUIRE(wg_x * wg_threads <= (int64_t)UINT32_MAX, "attention: too many workgroups (%d splits)", nsplit);
     return EXKV_OK;
 }
 

@@ -49,6 +49,13 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
     with pytest.raises(RuntimeError, match="split_len"):
         _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0, 0.1, None)
+    # grids past 2^32 work-items: 1024 splits x 4096 x 8 workgroups of 256 threads (head
+    # dim 64), 7M splits of 640-thread workgroups (head dim 128)
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 4096, 32, 8, 64, 16384, 16384, None, 0, 1024, 16, 0, 0.1, None)
+    assert rc == 1 and b"too many workgroups" in lib.exkv_last_error()
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 112000000, 112000000, None, 0, 7000000, 16, 0,
+                            0.1, None)
+    assert rc == 1 and b"too many workgroups" in lib.exkv_last_error()
     # paged entry points: a page table narrower than the pages to encode, a raw pool
     # without room for the tail areas, more rows than sequence slots
     rc = lib.exkv_encode_pages_paged(1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, None, 0, 1, 1, 1, 2, 1, 3, 4, 64, 128, None,

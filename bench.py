@@ -85,6 +85,16 @@ def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0, D=128):
     return total + 2 * B * Hq * D * 2
 
 
+MALL_BYTES = 256 << 20
+
+
+def rotation_copies(copy_bytes):
+    """Cache copies to rotate over: at least 4, and enough that the copies' compressed bytes
+    are twice the 256 MiB Infinity Cache, so that no call finds its cache there (c1's copies
+    are 53 MB each: 4 of them would fit)."""
+    return max(4, -(-2 * MALL_BYTES // int(copy_bytes)))
+
+
 def time_loop(fn, n, warmup, copies):
     """Average ms per call of fn(i) over n calls, rotating over `copies` inputs, timed with
     HIP events on the current stream (the stream every call launches on)."""
@@ -100,6 +110,21 @@ def time_loop(fn, n, warmup, copies):
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / n
+
+
+def settle(fns, copies, seconds=0.5):
+    """Run the calls untimed, in turn, until `seconds` of wall time have passed, so that the
+    GPU is at its steady clocks before the timed loops whatever --warmup is (a short warmup
+    leaves it below them: +1-3 us per call). Returns the number of calls made."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            for f in fns:
+                f(n % copies)
+            n += 1
+        torch.cuda.synchronize()
+    return n * len(fns)
 
 
 def time_calls(fn, n, warmup, copies):
@@ -162,10 +187,13 @@ def time_split_kernel(launch, n, warmup, copies):
     return sum(t) / n, t[n // 2]
 
 
-def time_graph(fn, n, warmup, copies, per_graph=20):
+def time_graph(fn, n, warmup, copies, per_graph=32):
     """Average ms per call of fn(i) with the calls captured in a HIP graph (per_graph calls
     rotating over `copies` inputs) and the graph replayed until n calls ran: the launch
-    path of a captured decode step, with no Python work between kernels. Workspaces are
+    path of a captured decode step, with no Python work between kernels. 32 calls per
+    graph are the attention calls of one 32-layer decode step (the engine captures a whole
+    step); each graph launch itself costs ~25 us on top of its calls, which graphs of 1-4
+    calls would charge to every call (c2a: +1.2-2 us per call). Workspaces are
     allocated by eager calls on the capture stream beforehand; timed with HIP events on
     the stream the graph is launched on."""
     import torch
@@ -250,7 +278,9 @@ def main():
                     help="the e2e model's shape (random init): c4's Llama-3.1-8B, or Llama-3.2-1B (head dim 64)")
     ap.add_argument("--e2e-work-gib", type=float, default=6.0,
                     help="memory kept free beyond the caches for activations, logits and pool growth")
-    ap.add_argument("--copies", type=int, default=4, help="cache copies rotated to defeat the 256 MB MALL")
+    ap.add_argument("--copies", type=int, default=None,
+                    help="cache copies rotated to defeat the 256 MB MALL (default: at least 4, and enough that "
+                         "the compressed copies of the attention shapes hold twice the MALL)")
     ap.add_argument("--cpu-runs", type=int, default=5, help="CPU baseline: median of this many runs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--target-blocks", type=int, default=None)
@@ -270,6 +300,8 @@ def main():
     if a.warmup is None:
         a.warmup = 200 if attn else 10
     if a.workload in ("e2e", "c3", "c2a_paged", "wire", "prefill", "e2e_paged", "cpu"):
+        if a.copies is None:
+            a.copies = 4
         if a.gpus != 1:
             print("bench.py measures one GPU", file=sys.stderr)
             sys.exit(2)
@@ -290,6 +322,8 @@ def main():
     torch.cuda.set_device(dev)
     B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
     D = a.head_dim
+    if a.copies is None:
+        a.copies = rotation_copies(2 * B * T * Hkv * D * 200.5 / 128)
     if D != 128:
         desc = f"{desc}, head dim {D}"
     # the c4 protocol's sequences-fit on this GPU, before the workload's data takes memory
@@ -331,6 +365,7 @@ def main():
     def full_b(i):
         kernels.attention_reference(q, kbs[i], vbs[i], T, nsplit=ns, split_len=sl, out=out, window=W)
 
+    settled = settle([full_c, full_b], a.copies)
     ms_c = time_loop(full_c, a.steps, a.warmup, a.copies)
     ms_b = time_loop(full_b, a.steps, a.warmup, a.copies)
     ms_split, ms_split_med = time_split_kernel(lambda i: split_only(kernels, q, kcs[i], vcs[i], T, ns, sl, True,
@@ -363,6 +398,7 @@ def main():
                      "kernel_timing": "HIP events recorded at each split kernel's own start and end "
                                       "(hipExtLaunchKernelGGL) on its launch stream, back-to-back launches"},
         "timing": "HIP events around back-to-back calls on one stream",
+        "settle_calls": settled,
         "graph_replay_us": round(ms_c_graph * 1e3, 2),
         "graph_replay_calls": max(a.steps, 200),
         "per_call_us": {"median": round(med * 1e3, 2), "p10": round(p10 * 1e3, 2), "p90": round(p90 * 1e3, 2),

@@ -88,11 +88,12 @@ def algorithmic_bytes(caches, B, T, Hq, Hkv, lens=None, window=0, D=128):
 MALL_BYTES = 256 << 20
 
 
-def rotation_copies(copy_bytes):
-    """Cache copies to rotate over: at least 4, and enough that the copies' compressed bytes
-    are twice the 256 MiB Infinity Cache, so that no call finds its cache there (c1's copies
-    are 53 MB each: 4 of them would fit)."""
-    return max(4, -(-2 * MALL_BYTES // int(copy_bytes)))
+def rotation_copies(read_bytes, most=16):
+    """Cache copies to rotate over: at least 4, and enough that the compressed bytes the calls
+    read add up to twice the 256 MiB Infinity Cache, so that no call finds its cache there
+    (c1 reads 53 MB per call: 4 copies would fit), but at most `most` (a short window reads
+    a few MB per call, which no practical rotation keeps out of the cache)."""
+    return min(most, max(4, -(-2 * MALL_BYTES // int(read_bytes))))
 
 
 def time_loop(fn, n, warmup, copies):
@@ -322,8 +323,8 @@ def main():
     torch.cuda.set_device(dev)
     B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
     D = a.head_dim
-    if a.copies is None:
-        a.copies = rotation_copies(2 * B * T * Hkv * D * 200.5 / 128)
+    if a.copies is None:                               # sized on the tokens a call reads (a window's only)
+        a.copies = rotation_copies(2 * B * (min(T, a.window + 15) if a.window else T) * Hkv * D * 200.5 / 128)
     if D != 128:
         desc = f"{desc}, head dim {D}"
     # the c4 protocol's sequences-fit on this GPU, before the workload's data takes memory

@@ -996,7 +996,7 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
         if (npw > 0) issue_raw(0, meta(0));
         if (npw > 1) issue_raw(1, meta(1));
 
-        progress[wave] = 0;
+        lds_flag_st(&progress[wave], 0);
         int stg = 0;                                   // stage of page j (j % NST)
         for (int j = 0; j < npw; ++j) {
             // page j's raw rows have landed once only page j + 1's are in flight
@@ -1015,8 +1015,8 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
             const bool valid = t0 + r < c.end && t0 + r >= c.wlo;
             const PageMeta mc = meta(j);
             const PageMeta mn = j + NST - 1 < npw ? meta(j + NST - 1) : PageMeta{0u, 0u, 0, 0};
-            const int other = progress[wave ^ 4];
-            progress[wave] = j;
+            const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
+            lds_flag_st(&progress[wave], j);
 
             // V first: its tile is written and its V^T operands read while K is rebuilt, so
             // that the stage goes back to the loader right after the score MFMAs
@@ -1118,7 +1118,7 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel<false>(AttnArgs a)
     load_qop(qst, r, g, c.gh, qop);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q is in registers before its stage is reused
 
-    progress[wave] = 0;
+    lds_flag_st(&progress[wave], 0);
     int stg = 0;
     for (int j = 0; j < npw; ++j) {
         wait_vm<0>();                                  // page j has landed (the only page in flight)
@@ -1134,8 +1134,8 @@ __global__ void __launch_bounds__(kThreads) attn_split_kernel<false>(AttnArgs a)
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             issue(j + NST - 1, ring + (uint32_t)(stn * STB));
         }
-        const int other = progress[wave ^ 4];
-        progress[wave] = j;
+        const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
+        lds_flag_st(&progress[wave], j);
         uint32_t kd[16];
         stage_bf16_k(sb, lo, kd);
         balance_priority(j, other);

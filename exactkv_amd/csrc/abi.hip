@@ -87,10 +87,12 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
 }
 
 // Split plan of the head-dim 64 / 256 kernels: their workgroups cover one KV head and one
-// group of 16 query heads; one round is 512 workgroups, two per CU (the GPU holds three at
-// head dim 64, two at 256, by their LDS rings) -- measured best at the c2a shape (B8 x 8192,
-// 32q/8kv): 8 splits at 64 (33.8 against 35.9 / 38.6 us for 16 / 32), 8 at 256 (94.0
-// against 95.5 / 109.2 us). Head dim 128: the plan of exkv_plan_splits with its defaults.
+// group of 16 query heads. Rounds are counted in 512 workgroups, two per CU (the GPU holds
+// three at head dim 64, two at 256, by their LDS rings); with fewer units than that, head
+// dim 64 fills all three slots of every CU (768 workgroups). Measured at the c2a shape (B8 x
+// 8192, 32q/8kv, split kernel): at 64, 12 splits 32.1 us against 33.0 / 34.9 / 34.5 for 8 /
+// 16 / 24; at 256, 8 splits 88.3 us against 153.1 / 95.0 for 4 / 16. Head dim 128: the plan
+// of exkv_plan_splits with its defaults.
 extern "C" int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t D, int32_t* nsplit,
                                    int32_t* split_len) {
     EXKV_REQUIRE(exkv::head_dim_ok(D), "plan_splits_hd: head dim must be 64, 128 or 256 (got %d)", D);
@@ -98,6 +100,6 @@ extern "C" int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T
     EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits_hd: bad arguments");
     EXKV_REQUIRE(nsplit && split_len, "plan_splits_hd: null output");
     const int64_t units = (int64_t)B * Hkv * ((Hq / Hkv + 15) / 16);
-    plan_core(units, T, 512, 64, nsplit, split_len);
+    plan_core(units, T, D == 64 && units < 512 ? 768 : 512, 64, nsplit, split_len);
     return EXKV_OK;
 }

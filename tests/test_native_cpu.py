@@ -94,9 +94,9 @@ def test_plan_splits(B, Hkv, Hq, T, expect):
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,D,expect", [
-    (8, 8, 32, 8192, 64, (8, 1024)),     # 64 units (one per KV head) x 8 = 512 workgroups (two per CU)
-    (8, 8, 32, 8192, 256, (8, 1024)),
-    (32, 2, 14, 4096, 64, (8, 512)),     # Qwen2.5-0.5B shape: 64 units
+    (8, 8, 32, 8192, 64, (12, 704)),     # 64 units (one per KV head) x 12 = 768 workgroups (three per CU)
+    (8, 8, 32, 8192, 256, (8, 1024)),    # 64 units x 8 = 512 workgroups (two per CU)
+    (32, 2, 14, 4096, 64, (12, 352)),    # Qwen2.5-0.5B shape: 64 units
     (1, 8, 32, 131072, 256, (64, 2048)),
     (2, 2, 64, 1000, 64, (16, 64)),      # G = 32: two head groups per KV head, 8 units; capped by 64-token splits
     (600, 8, 32, 4096, 64, (2, 2048)),   # 4800 units, 9.4 rounds: two splits fill the last round to 98.7%

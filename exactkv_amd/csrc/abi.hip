@@ -31,9 +31,12 @@ extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 // Split plan for MI355X: about target_blocks workgroups in total over B * (Hkv / HW) * head
 // groups, where a workgroup covers HW = gcd(Hkv, 8) KV heads -- 256 by default, one per
 // CU, since a workgroup holds ~150 KB of LDS -- with
-// at least min_split tokens per split (64 by default: a wavefront's pages follow one
-// another at about one memory round trip each, so a few units are served best by many
-// short splits) and a split length that is a multiple of 32. Plays the role of the reference's choose_split
+// at least min_split tokens per split (16 by default, one page: a wavefront's pages follow
+// one another at about one memory round trip each, so a few units are served best by many
+// short splits; measured with one round of workgroups, 64- / 32- / 16-token splits: a
+// 1024-token window of one B1 x 128K sequence 14.2 / 11.1 / 9.6 us, B8 x 1024 15.8 / 14.7
+// us, B1 x 8192 16.1 / 14.3 us) and a split length that is a multiple of 32, or 16. Plays
+// the role of the reference's choose_split
 // (kernels.py:273-277), which targets 512 programs for a 128-SM-class GPU.
 // The split count for `units` workgroup units: up to target_blocks units, one round of
 // about target_blocks workgroups; more units than that: the fewest splits that give at
@@ -64,7 +67,7 @@ static void plan_core(int64_t units, int32_t T, int64_t target_blocks, int32_t m
     if (ns > cap) ns = cap;
     if (ns < 1) ns = 1;
     int64_t sl = ((int64_t)T + ns - 1) / ns;
-    sl = (sl + 31) / 32 * 32;
+    sl = sl <= exkv::kPage ? exkv::kPage : (sl + 31) / 32 * 32;
     *split_len = (int32_t)sl;
     *nsplit = (int32_t)(((int64_t)T + sl - 1) / sl);
 }
@@ -74,7 +77,7 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
     EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits: bad arguments");
     EXKV_REQUIRE(nsplit && split_len, "plan_splits: null output");
     if (target_blocks <= 0) target_blocks = 256;
-    if (min_split <= 0) min_split = 64;
+    if (min_split <= 0) min_split = exkv::kPage;
     const int64_t hg = (Hq / Hkv + 15) / 16;
     int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8)
     while (m) {

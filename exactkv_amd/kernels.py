@@ -41,13 +41,13 @@ def plan_splits_hd(B, Hkv, Hq, T, D):
     return ns.value, sl.value
 
 
-def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=64):
-    """MI355X split plan (native): about `target_blocks` workgroups (one per CU) -- or about
-    8x that many when there are more (sequence, head-block) units than workgroups in one
-    round -- at least `min_split` tokens per split, split length a multiple of 32.
+def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=16):
+    """MI355X split plan (native): about `target_blocks` workgroups (one per CU) when there
+    are fewer (sequence, head-block) units than that, else at least two full rounds -- at
+    least `min_split` tokens per split, split length a multiple of 32 (or one 16-token page).
     Returns (nsplit, split_len). Short splits cost little: a wavefront's pages follow one
     another at about one round trip each, so few units are best served by many splits
-    (measured: B1 x 8K 36 -> 18 us, B4 x 1K 35 -> 16 us going from 256- to 64-token splits)."""
+    (measured: B1 x 8K 36 -> 18 -> 14.3 us going from 256- to 64- to 32-token splits)."""
     ns, sl = ctypes.c_int32(), ctypes.c_int32()
     _lib.call("exkv_plan_splits", B, Hkv, Hq, T, target_blocks, min_split, ctypes.byref(ns), ctypes.byref(sl))
     return ns.value, sl.value

@@ -105,6 +105,23 @@ def test_split_plans(T, ns_sl):
             assert same_bits(f_c, o_c)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,T", [(1, 28, 4, 1000), (2, 8, 1, 777), (4, 32, 8, 500), (1, 32, 8, 8192)])
+def test_default_plans_of_small_grids(B, Hq, Hkv, T):
+    """Grids smaller than the GPU take splits down to one page (the default plan): with 4 or
+    fewer KV heads per workgroup the later page phases of a one-page split have no page."""
+    q, k, v = _ref_case(B, T, Hq, Hkv, seed=11)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    ns, sl = kernels.plan_splits(B, Hkv, Hq, T)
+    _say("default plan", B, Hq, Hkv, T, ns, sl)
+    assert sl <= 32
+    o_c = kernels.attention_compressed(qd, kc, vc, T)
+    o_r = kernels.attention_reference(qd, kd, vd, T)
+    assert same_bits(o_c, o_r)
+    assert same_bits(o_c, kernels.attention_compressed(qd, kc, vc, T, nsplit=ns, split_len=sl))
+    assert_bf16_tolerance(o_c, oatt.attention(u16(q), u16(k), u16(v), T, np.float32))
+
+
 def test_synthetic_keys_with_raw_rows_and_zero_groups():
     """Config-0 style K/V (RoPE'd keys, 0.04% zeros, 0.3% raw rows) at 32q/8kv."""
     B, T, Hq, Hkv = 2, 2048 - 7, 32, 8

@@ -78,9 +78,9 @@ def test_argument_errors_are_reported_without_launching():
     (1, 8, 32, 131072, (256, 512)),
     (1, 4, 28, 32768, (256, 128)),     # 4 KV heads per workgroup: one unit, 256 splits
     (32, 8, 32, 4096, (8, 512)),
-    (1, 4, 28, 8000, (125, 64)),       # capped by min_split 64
-    (4, 2, 16, 17, (1, 32)),
-    (2, 2, 64, 1000, (16, 64)),        # G = 32: two head groups per KV head
+    (1, 4, 28, 8000, (250, 32)),       # one unit: 256 splits of at least a page, rounded to 32 tokens
+    (4, 2, 16, 17, (2, 16)),           # capped by one page per split
+    (2, 2, 64, 1000, (63, 16)),        # G = 32: two head groups per KV head, 4 units; one page per split
     (620, 8, 32, 4352, (2, 2176)),     # more units than one round: >= 2 rounds, the last >= 95% full (4.84 rounds)
     (256, 8, 32, 4096, (2, 2048)),     # exactly two rounds
     (300, 8, 32, 4096, (5, 832)),      # 5.86 rounds: the first split count whose last round is >= 95% full
@@ -90,7 +90,7 @@ def test_plan_splits(B, Hkv, Hq, T, expect):
     from exactkv_amd.kernels import plan_splits
     ns, sl = plan_splits(B, Hkv, Hq, T)
     assert (ns, sl) == expect
-    assert sl % 32 == 0 and ns * sl >= T and (ns - 1) * sl < T
+    assert (sl % 32 == 0 or sl == 16) and ns * sl >= T and (ns - 1) * sl < T
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,D,expect", [

@@ -308,7 +308,7 @@ int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_
                          int32_t window, float qk_scale, hipStream_t stream);
 
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
- * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 64), split_len a multiple of 32.
+ * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 16, one page), split_len a multiple of 32 or 16.
  * Replaces: kernels.py:273-277 choose_split. */
 int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);

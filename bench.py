@@ -12,6 +12,10 @@ dominant kernel (the split kernel: algorithmic bytes / its average duration, HIP
 the launch stream), the bf16-uncompressed twin for comparison, the encoder's throughput,
 and the CPU baseline (the reference codec restated in PyTorch decoding both caches, then
 fp32 attention, on every host core this process may use; median of full calls).
+The default line also carries the metric's second half, `e2e`: c4 greedy decode tok/s of
+both caches (random-init Llama-3.1-8B, 4096-token prompts, 256 tokens, each cache at the
+largest batch its KV budget holds), from `--workload e2e --e2e-rows own` run first as a
+child process (about 2.5 minutes; --no-e2e leaves it out).
 --workload cpu times that baseline at every benchmark shape without the GPU.
 
     python bench.py [--steps 400] [--warmup 200] [--workload c2a]
@@ -279,6 +283,14 @@ def main():
                     help="the e2e model's shape (random init): c4's Llama-3.1-8B, or Llama-3.2-1B (head dim 64)")
     ap.add_argument("--e2e-work-gib", type=float, default=6.0,
                     help="memory kept free beyond the caches for activations, logits and pool growth")
+    ap.add_argument("--e2e-rows", default="all", choices=("all", "own"),
+                    help="e2e runs: 'own' = each cache at its own largest batch; 'all' adds the compressed cache "
+                         "at the bf16 batch (same work: step-time ratio and token identity)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="default line without its e2e leg (c4 decode tok/s of both caches, run first as a child "
+                         "process: about 2.5 minutes)")
+    ap.add_argument("--e2e-timeout", type=float, default=420.0,
+                    help="seconds the default line's e2e child may take before it is stopped and reported as such")
     ap.add_argument("--copies", type=int, default=None,
                     help="cache copies rotated to defeat the 256 MB MALL (default: at least 4, and enough that "
                          "the compressed copies of the attention shapes hold twice the MALL)")
@@ -315,20 +327,22 @@ def main():
               "(the decode path shards by KV head or sequence with no exchange)", file=sys.stderr)
         sys.exit(2)
 
+    B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
+    D = a.head_dim
+    default_line = a.workload == "c2a" and D == 128 and not a.window and not a.profile and not a.target_blocks
+
     import torch
     import exactkv_amd as exactkv
     from exactkv_amd import kernels, synthetic
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    B, T, TS, Hq, Hkv, desc = WORKLOADS[a.workload]
-    D = a.head_dim
     if a.copies is None:                               # sized on the tokens a call reads (a window's only)
         a.copies = rotation_copies(2 * B * (min(T, a.window + 15) if a.window else T) * Hkv * D * 200.5 / 128)
     if D != 128:
         desc = f"{desc}, head dim {D}"
     # the c4 protocol's sequences-fit on this GPU, before the workload's data takes memory
-    fit = e2e_fit() if a.workload == "c2a" and D == 128 and not a.window and not a.profile else None
+    fit = e2e_fit() if default_line else None
     print(f"[bench] {a.workload}: {desc}; generating data", file=sys.stderr, flush=True)
     k = synthetic.make_kv(B, TS, Hkv, D=D, kind="k", seed=100, device=dev)
     v = synthetic.make_kv(B, TS, Hkv, D=D, kind="v", seed=101, device=dev)
@@ -418,6 +432,14 @@ def main():
         print("[bench] cpu baseline timed", file=sys.stderr, flush=True)
     if fit is not None:
         res["e2e_fit"] = fit
+    if default_line and not a.no_e2e:
+        # the metric's second half, c4 decode tok/s of both caches, last (two minutes of full
+        # load before the attention timing would leave the GPU warmer than the other lines)
+        del kcs, vcs, kbs, vbs, q, out, o_c, o_r
+        kernels.release_workspaces()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        res["e2e"] = e2e_child(a)
     print(json.dumps(res), flush=True)
 
 
@@ -782,6 +804,38 @@ E2E_CONFIG_1B = dict(vocab_size=128256, hidden_size=2048, intermediate_size=8192
 E2E_MODELS = {"llama3.1-8b": ("Llama-3.1-8B", E2E_CONFIG), "llama3.2-1b": ("Llama-3.2-1B (head dim 64)", E2E_CONFIG_1B)}
 
 
+def e2e_child(a):
+    """The default line's e2e leg: `bench.py --workload e2e --e2e-rows own` (c4: each cache at
+    its own largest batch, 4096-token prompts, 256 greedy tokens) as a child process with a
+    time limit, started once this process has freed its tensors (it keeps only its HIP
+    context, so the child's KV budget is a few hundred MB below a fresh process's). Its
+    progress goes to stderr; its JSON line is summarised here."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--workload", "e2e", "--e2e-rows", "own",
+           "--e2e-prompt", str(a.e2e_prompt), "--e2e-gen", str(a.e2e_gen)]
+    print(f"[bench] e2e leg: {' '.join(cmd[1:])}", file=sys.stderr, flush=True)
+    t0 = time.time()
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=a.e2e_timeout)
+    except subprocess.TimeoutExpired:
+        return {"error": f"stopped after {a.e2e_timeout:.0f} s", "command": " ".join(cmd[1:])}
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"error": f"exit status {r.returncode}", "command": " ".join(cmd[1:])}
+    d = json.loads(lines[-1])
+    rows = {row["backend"]: row for row in d["rows"]}
+    b, c = rows["bf16"], rows["exactkv"]
+    print("[bench] e2e leg done", file=sys.stderr, flush=True)
+    return {"workload": d["config"]["workload"], "metric": "decode tok/s = B * (gen - 1) / decode wall time",
+            "tok_s": {"bf16": b["decode_tokens_per_s"], "exactkv": c["decode_tokens_per_s"]},
+            "ratio": d["throughput_ratio"], "batch": {"bf16": b["batch"], "exactkv": c["batch"]},
+            "sequences_fit": d["config"]["sequences_fit"],
+            "ms_per_step": {"bf16": b["ms_per_step"], "exactkv": c["ms_per_step"]},
+            "prefill_s": {"bf16": b["prefill_s"], "exactkv": c["prefill_s"]},
+            "prompt": d["config"]["prompt"], "gen": d["config"]["gen"], "wall_s": round(time.time() - t0, 1),
+            "command": " ".join(cmd[1:])}
+
+
 def e2e_fit(model_key="llama3.1-8b", prompt=4096, gen=256):
     """The sequences-fit half of the c4 protocol (reference bench/e2e.py:54-63), measured
     without running the model: a placeholder of the model's weight bytes (the parameter
@@ -1010,7 +1064,7 @@ def e2e(a):
 
     r_b, tok_b = run("bf16", run_b["bf16"])
     r_c, tok_c = run("exactkv", run_b["exactkv"])
-    r_s, tok_s = run("exactkv", r_b["batch"])
+    r_s, tok_s = run("exactkv", r_b["batch"]) if a.e2e_rows == "all" else (None, None)
     res = {
         "metric": f"e2e greedy decode tok/s ({mname} random init, {PL}-token prompts, {G} new tokens)",
         "value": r_c["decode_tokens_per_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
@@ -1019,12 +1073,13 @@ def e2e(a):
                    "prompt": PL, "gen": G, "head_dim": mcfg["hidden_size"] // mcfg["num_attention_heads"],
                    "weights_gib": round(wbytes / 2**30, 2), "kv_budget_gib": round(budget / 2**30, 2),
                    "sequences_fit": fit, "batch_run": run_b},
-        "rows": [r_b, r_c, r_s],
+        "rows": [r for r in (r_b, r_c, r_s) if r is not None],
         "throughput_ratio": round(r_c["decode_tokens_per_s"] / r_b["decode_tokens_per_s"], 3),
-        "step_time_ratio_same_batch": round(r_b["ms_per_step"] / r_s["ms_per_step"], 3),
-        "tokens_equal_same_batch": bool(torch.equal(tok_b, tok_s)),
         "gpu": torch.cuda.get_device_name(0),
     }
+    if r_s is not None:
+        res["step_time_ratio_same_batch"] = round(r_b["ms_per_step"] / r_s["ms_per_step"], 3)
+        res["tokens_equal_same_batch"] = bool(torch.equal(tok_b, tok_s))
     print(json.dumps(res), flush=True)
 
 

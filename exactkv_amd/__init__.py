@@ -1,6 +1,7 @@
-"""exactkv on MI355X: a lossless (bit-exact) compressed KV cache for LLM decoding, with
-decode attention that reads the compressed cache directly -- hand-written HIP kernels
-for gfx950 behind the reference's Python API (drop-in for zyfyz666/exactkv's names).
+"""exactkv_amd: keys and values of a decoding LLM held in exactkv's compressed page format
+(every bf16 bit kept), with a gfx950 decode-attention kernel that rebuilds pages on the fly
+from that format. All kernels are hand-written HIP behind the reference's Python names, so
+code written against zyfyz666/exactkv runs unchanged.
 
     import exactkv_amd as exactkv
 """

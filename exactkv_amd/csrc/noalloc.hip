@@ -4,9 +4,13 @@
 //
 // The array is a file-scope __device__ object, so every GPU the library runs on holds its
 // own copy for the life of the process. Host code never uses its name as an address: the
-// first call on a device (with that device current) asks the runtime for the device's
-// address once (hipGetSymbolAddress) and keeps it. Every call on a GPU shares that GPU's
-// array; calls that overlap on one GPU (other streams, other threads) race on it.
+// first call on a device asks the runtime for that device's address (hipGetSymbolAddress,
+// with the device current) and keeps it. The device is the one the call's stream belongs
+// to (hipStreamGetDevice), not whichever device happens to be current, so a call on another
+// GPU's stream gets that GPU's array. A failed lookup is not kept: the next call on the
+// device asks again. Every call on a GPU shares that GPU's array; calls that overlap on one
+// GPU (other streams, other threads) race on it.
+#include <atomic>
 #include <mutex>
 
 #include "common.hpp"
@@ -19,24 +23,43 @@ constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-static void* g_scratch[kMaxDevices];
-static hipError_t g_scratch_rc[kMaxDevices];
-static std::once_flag g_scratch_once[kMaxDevices];
+static std::atomic<void*> g_scratch[kMaxDevices];      // nullptr until a lookup succeeds
+static std::mutex g_scratch_mu;
 
-// The current device's copy of the scratch array (looked up once per device).
-static int scratch_of_current_device(float** out) {
-    int dev = -1;
-    const hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_status(e, "attn_compressed_noalloc: hipGetDevice");
-    EXKV_REQUIRE(dev >= 0 && dev < kMaxDevices, "attn_compressed_noalloc: device %d out of range", dev);
-    std::call_once(g_scratch_once[dev], [dev]() {
-        void* p = nullptr;
-        g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        g_scratch[dev] = p;
-    });
-    if (g_scratch_rc[dev] != hipSuccess) return hip_status(g_scratch_rc[dev], "attn_compressed_noalloc: hipGetSymbolAddress");
-    EXKV_REQUIRE(g_scratch[dev] != nullptr, "attn_compressed_noalloc: no scratch address for device %d", dev);
-    *out = static_cast<float*>(g_scratch[dev]);
+// The device of `stream` (the null stream: the current device).
+static int stream_device(hipStream_t stream, int* dev) {
+    hipDevice_t d = -1;
+    const hipError_t e = hipStreamGetDevice(stream, &d);
+    if (e != hipSuccess) return hip_status(e, "attn_compressed_noalloc: hipStreamGetDevice");
+    EXKV_REQUIRE(d >= 0 && d < kMaxDevices, "attn_compressed_noalloc: device %d out of range", (int)d);
+    *dev = (int)d;
+    return EXKV_OK;
+}
+
+// Device dev's copy of the scratch array. The lookup runs with dev current (the caller's
+// current device is restored afterwards) and is kept only once it has succeeded.
+static int scratch_of_device(int dev, float** out) {
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            int cur = -1;
+            hipError_t e = hipGetDevice(&cur);
+            if (e != hipSuccess) return hip_status(e, "attn_compressed_noalloc: hipGetDevice");
+            if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+                return hip_status(e, "attn_compressed_noalloc: hipSetDevice");
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (cur != dev) {
+                const hipError_t r = hipSetDevice(cur);
+                if (e == hipSuccess && r != hipSuccess) e = r;
+            }
+            if (e != hipSuccess) return hip_status(e, "attn_compressed_noalloc: hipGetSymbolAddress");
+            EXKV_REQUIRE(p != nullptr, "attn_compressed_noalloc: no scratch address for device %d", dev);
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = static_cast<float*>(p);
     return EXKV_OK;
 }
 
@@ -59,8 +82,11 @@ extern "C" int exkv_attn_compressed_noalloc(const void* q, const void* k_sm, con
     EXKV_REQUIRE(need <= exkv::kScratchBytes,
                  "attn_compressed_noalloc: %lld split partials need %lld bytes, more than the %lld-byte scratch",
                  (long long)partials, (long long)need, (long long)exkv::kScratchBytes);
+    int dev = -1;
+    int rc = exkv::stream_device(stream, &dev);
+    if (rc != EXKV_OK) return rc;
     float* s = nullptr;
-    const int rc = exkv::scratch_of_current_device(&s);
+    rc = exkv::scratch_of_device(dev, &s);
     if (rc != EXKV_OK) return rc;
     float* ws_o = s;                                                // [B*Hq, nsplit, D]
     float* ws_m = ws_o + partials * D;                              // [B*Hq, nsplit]

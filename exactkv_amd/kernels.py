@@ -83,6 +83,15 @@ FUSED_MERGE_MAX_SPLITS = 1024   # up to this many splits the split kernel can me
 # delays the workgroups queued behind it, while the separate merge adds 1.5 us at c2a.
 
 
+def release_workspaces():
+    """Drop every cached workspace (split partials, arrival counters, scan workspaces), so
+    that torch's allocator can return their memory; later calls allocate new ones (the
+    counters and scan workspaces zeroed, as on first use)."""
+    _WS.clear()
+    _CNT.clear()
+    _SCAN.clear()
+
+
 def _counters(dev, n):
     key = (dev.index, _lib.stream(), n)
     c = _CNT.get(key)
@@ -233,6 +242,11 @@ def attention_compressed_noalloc(q, kc, vc, T, *, out, lens=None, nsplit=None, s
         raise ValueError("k and v caches differ in shape or hold fewer sequences than q")
     if _cache_dim(kc) != D or _cache_dim(vc) != D:
         raise ValueError(f"cache head dim {_cache_dim(kc)} / {_cache_dim(vc)} differs from q's {D}")
+    # the library uses the scratch array of the GPU the stream belongs to: q's
+    held = [t for c in (kc, vc) for t in ((c["sm"], c["raw"]) if isinstance(c, dict) else (c.sm, c.raw))]
+    others = [t for t in (out, lens, *held) if isinstance(t, torch.Tensor)]
+    if any(t.device != q.device for t in others):
+        raise ValueError(f"q, out, the caches and lens must all be on {q.device}")
     window = _window_arg(window)
     ns, sl = _plan(B, Hkv, Hq, T, TS, lens, nsplit, split_len, window, D)
     lp, lstride = _lens_arg(lens, B)

@@ -7,7 +7,8 @@
  * Conventions
  *   - All pointers are device pointers (HIP), except the outputs of the split planners.
  *   - Work is enqueued on `stream` only; nothing synchronizes, nothing allocates, so
- *     calls can be captured in a HIP graph. The library holds no device state.
+ *     calls can be captured in a HIP graph. The library's one piece of device state is
+ *     exkv_attn_compressed_noalloc's fixed scratch array on each GPU it runs on.
  *   - bf16 tensors are passed as raw 16-bit patterns. Tensors are row-major with the
  *     shapes given; "elements" strides count bf16 elements.
  *   - Return value: 0 ok, 1 invalid argument, 2 HIP launch error; exkv_last_error()
@@ -70,7 +71,7 @@ int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_pg, int64_t 
                             const int32_t* dst_pages, int64_t dst_stride, int32_t nb, int32_t npg, int32_t H,
                             int32_t TS, int32_t D, void* scan_ws, int64_t scan_ws_words, hipStream_t stream);
 
-/* Append one token per sequence (x: [B, H, 128] bf16, row strides sx_b, sx_h) to the cache
+/* Append one token per sequence (x: [B, H, D] bf16, row strides sx_b, sx_h) to the cache
  * whose token count is state[0] (device): write it into the tail area; when it completes
  * page T/16, encode that page (slots as above, *before = counter before) and open the next
  * page (rowmask 0xFFFF, rowoff into the tail area); then state[0] += 1. Nothing is written
@@ -81,13 +82,13 @@ int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void*
                       int32_t* state, int64_t cap, int64_t raw_rows, int32_t B, int32_t H, int32_t TS,
                       int32_t D, hipStream_t stream);
 
-/* Append to a plain bf16 cache buf [B, TS, H, 128] at position state[0]; state[0] += 1.
+/* Append to a plain bf16 cache buf [B, TS, H, D] at position state[0]; state[0] += 1.
  * Replaces: cache.py:141-143 BF16KV.append. */
 int exkv_bf16_append(const void* x, int64_t sx_b, int64_t sx_h, void* buf, int32_t* state, int32_t B,
                      int32_t H, int32_t TS, int32_t D, hipStream_t stream);
 
 /* Append one token for each of n sequences of a paged cache: a pool of pool_pages pages
- * (arrays as a [1, 16 * pool_pages, H, 128] cache) shared by max_seqs sequence slots.
+ * (arrays as a [1, 16 * pool_pages, H, D] cache) shared by max_seqs sequence slots.
  * Batch row i is slot slots[i] (slots == NULL: slot i; the slots must differ); slot s owns
  * pool pages block_table[s * bt_stride + pg] (pg < max_pages, entries clamped to the
  * pool) and holds lens[s] tokens, the new one included (the caller raises lens first; the
@@ -105,7 +106,7 @@ int exkv_cache_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* sm,
                             int32_t max_seqs, int32_t max_pages, int32_t pool_pages, int32_t D,
                             hipStream_t stream);
 
-/* bf16 twin of exkv_cache_append_paged over a pool buf [16 * pool_pages, H, 128]: token
+/* bf16 twin of exkv_cache_append_paged over a pool buf [16 * pool_pages, H, D]: token
  * lens[s] - 1 of slot s goes to row (block_table[s, t / 16] * 16 + t % 16).
  * No counterpart in the reference (see exkv_cache_append_paged). */
 int exkv_bf16_append_paged(const void* x, int64_t sx_b, int64_t sx_h, void* buf, const int32_t* slots,
@@ -188,13 +189,13 @@ int exkv_wire_unpack(void* sm, void* code, void* base, int32_t* rowmask, int32_t
                      const int64_t* tail_rows, const uint64_t* blobs, const int64_t* blob_bytes,
                      int32_t max_tokens, int32_t H, int32_t D, int32_t* ws, int64_t ws_stride, hipStream_t stream);
 
-/* Compressed cache -> bf16 out [B, T, H, 128] through the attention kernels' page decoder.
+/* Compressed cache -> bf16 out [B, T, H, D] through the attention kernels' page decoder.
  * Replaces: kernels.py:331-337 decode_to_bf16 (_dec_only_kernel :197-211). */
 int exkv_decode_to_bf16(const void* sm, const void* code, const void* base, const int32_t* rowmask,
                         const int32_t* rowoff, const void* raw, int64_t raw_rows, void* out, int32_t B,
                         int32_t T, int32_t TS, int32_t H, int32_t D, hipStream_t stream);
 
-/* decode_to_bf16 over a paged cache (arrays of pool_pages pages): out [B, T, H, 128] holds
+/* decode_to_bf16 over a paged cache (arrays of pool_pages pages): out [B, T, H, D] holds
  * tokens [0, T) of each sequence b, page p read from pool page block_table[b*bt_stride + p]
  * (entries clamped to the pool; T <= 16*bt_stride). No counterpart in the reference
  * (contiguous caches only; paged KV is in its future work, README.md:121-123). */
@@ -204,7 +205,7 @@ int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base
                               int32_t H, int32_t D, hipStream_t stream);
 
 /* Split-K GQA decode attention over compressed K and V caches, then the split merge.
- * q [B, Hq, 128] bf16; out [B, Hq, 128] bf16; workspace ws_o [B*Hq, nsplit, 128],
+ * q [B, Hq, D] bf16; out [B, Hq, D] bf16; workspace ws_o [B*Hq, nsplit, D],
  * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: exkv_merge_counters(B, Hq, Hkv, nsplit) i32
  * arrival counters, all zero before the first call (each call leaves them zero). With
  * ws_cnt (and nsplit <= 1024) the merge runs inside the split kernel: the last workgroups
@@ -212,7 +213,8 @@ int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base
  * the separate merge's bits, up to 8 splits); without it, as a second kernel. Calls that
  * share a workspace must not overlap.
  * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
- * when lens != NULL (then nsplit*split_len must cover TS). split_len: multiple of 32.
+ * when lens != NULL (then nsplit*split_len must cover TS). split_len: a positive multiple
+ * of 16.
  * window > 0 (sliding-window attention): only the last `window` of those tokens,
  * [len - window, len); the splits then start at that range's first page, so they need
  * to cover only min(T or TS, window + 15) tokens. window = 0: all tokens. (Additive: the
@@ -233,9 +235,12 @@ int exkv_attn_compressed(const void* q, const void* k_sm, const void* k_code, co
  * allocate (code under HIP-graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The split partials go to a fixed scratch
  * array in device memory that the library holds on every GPU it runs on, for the life of
- * the process: at most exkv_noalloc_scratch_bytes() (32 MiB) = B * Hq * nsplit * 130 * 4
- * bytes, so B * Hq * nsplit <= 64,527; larger calls return 1 with a message. The merge runs
- * as the second kernel. Call with the stream's device current. Every call on one GPU shares
+ * the process: B * Hq * nsplit partials of (D + 2) floats must fit its
+ * exkv_noalloc_scratch_bytes() (32 MiB), i.e. B * Hq * nsplit <= floor(32 MiB / ((D + 2) * 4)):
+ * 127,100 at D = 64, 64,527 at D = 128, 32,513 at D = 256; larger calls return 1 with a
+ * message. The merge runs as the second kernel. The array used is that of the GPU `stream`
+ * belongs to (all tensors must live there); the first call on a GPU looks its address up
+ * (not under stream capture: make one call before capturing). Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (other streams or threads) race. Same
  * arguments otherwise, and the same bits as exkv_attn_compressed. */
 int exkv_attn_compressed_noalloc(const void* q, const void* k_sm, const void* k_code, const void* k_base,
@@ -249,7 +254,7 @@ int exkv_attn_compressed_noalloc(const void* q, const void* k_sm, const void* k_
 /* Size in bytes of exkv_attn_compressed_noalloc's per-GPU scratch array. */
 int64_t exkv_noalloc_scratch_bytes(void);
 
-/* The same attention over plain bf16 caches k, v [B, TS, Hkv, 128].
+/* The same attention over plain bf16 caches k, v [B, TS, Hkv, D].
  * Replaces: kernels.py:321-328 attention_reference (_split_ref_kernel :168-194). */
 int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, float* ws_m, float* ws_l,
                    int32_t* ws_cnt, void* out, int32_t B, int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t TS,
@@ -258,7 +263,7 @@ int exkv_attn_bf16(const void* q, const void* k, const void* v, float* ws_o, flo
 
 /* The two phases of exkv_attn_compressed / exkv_attn_bf16 separately: the split kernel
  * (partials into ws_o, ws_m, ws_l) and the merge of `nsplit` partials per row into
- * out [rows, 128] bf16 (rows = B*Hq).
+ * out [rows, D] bf16 (rows = B*Hq).
  * Replaces: the _split_c_kernel / _split_ref_kernel launches (kernels.py:316-317, :325-327)
  * and kernels.py:295-299 _reduce (_reduce_kernel :33-43). */
 int exkv_attn_split_compressed(const void* q, const void* k_sm, const void* k_code, const void* k_base,
@@ -308,7 +313,8 @@ int exkv_attn_bf16_paged(const void* q, const void* k, const void* v, float* ws_
                          int32_t window, float qk_scale, hipStream_t stream);
 
 /* Host-side split plan for MI355X (host pointers out): about target_blocks workgroups
- * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 16, one page), split_len a multiple of 32 or 16.
+ * (<= 0: 256, one per CU), at least min_split tokens per split (<= 0: 16, one page), split_len
+ * a multiple of 32, or 16.
  * Replaces: kernels.py:273-277 choose_split. */
 int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t target_blocks,
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);

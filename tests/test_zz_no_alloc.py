@@ -57,3 +57,27 @@ def test_noalloc_rejects_plans_beyond_the_scratch():
         kernels.attention_compressed_noalloc(q, kc, vc, 8192, out=out, nsplit=512, split_len=16)
     with pytest.raises(ValueError, match="out"):
         kernels.attention_compressed_noalloc(q, kc, vc, 512, out=None)
+
+
+def test_noalloc_replays_from_a_hip_graph():
+    """The call's use case: captured in a HIP graph (no allocation inside the capture) and
+    replayed. The first call on the GPU (which looks the scratch address up) runs eagerly,
+    then three replays with new queries written in place between them, each checked against
+    the workspace call run eagerly after it."""
+    print("[case] noalloc graph replay", flush=True)
+    B, T, Hq, Hkv = 8, 4096, 32, 8
+    q, kc, vc = _case(B, T, Hq, Hkv, seed=331)
+    out = torch.empty_like(q)
+    kernels.attention_compressed_noalloc(q, kc, vc, T, out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernels.attention_compressed_noalloc(q, kc, vc, T, out=out)
+    for i in range(3):
+        q.copy_(synthetic.make_q(B, Hq, seed=340 + i).to(DEV))
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        want = kernels.attention_compressed(q, kc, vc, T)
+        torch.cuda.synchronize()
+        assert same_bits(out, want), i

@@ -9,7 +9,10 @@ import os
 
 # EXACTKV_LIB overrides the path of the library to load (default: the in-tree build)
 _PATH = os.environ.get("EXACTKV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libexactkv_hip.so")
-ABI_VERSION = 3
+# EXACTKV_CHECK_ERRORS=1: after every kernel-launching call, wait for its stream and raise if
+# a kernel set a sticky error bit (exkv_error_bits); slow, for debugging
+_CHECK = os.environ.get("EXACTKV_CHECK_ERRORS", "") not in ("", "0")
+ABI_VERSION = 4
 
 _p, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 
@@ -60,6 +63,8 @@ SIGNATURES = {
     "exkv_plan_splits_hd": [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "exkv_abi_version": [],
     "exkv_last_error": [],
+    "exkv_error_bits": [_p, _i32, _p],
+    "exkv_set_wait_limit": [_i32],
 }
 
 _lib = None
@@ -95,6 +100,28 @@ def load():
     return lib
 
 
+# entry points that take no stream (host-only, or hooks)
+_NO_STREAM = {"exkv_wire_bytes", "exkv_time_next_split", "exkv_merge_counters", "exkv_noalloc_scratch_bytes",
+              "exkv_plan_splits", "exkv_plan_splits_hd", "exkv_abi_version", "exkv_last_error", "exkv_error_bits",
+              "exkv_set_wait_limit"}
+
+# error bit -> what a kernel reports with it (include/exactkv.h EXKV_ERR_*)
+ERROR_BITS = {
+    0x1: "attention: a wait on another wavefront's LDS flag gave up",
+    0x2: "attention / decode: a raw row's pool slot lay outside the pool (clamped)",
+    0x4: "encoder: the slot scan's look-back gave up on a predecessor",
+    0x8: "encoder: inconsistent scan workspace",
+    0x10: "wire pack: a raw row's pool slot lay outside the pool (clamped)",
+}
+
+
+def describe_errors(bits):
+    """The EXKV_ERR_* bits of `bits` in words."""
+    names = [msg for b, msg in ERROR_BITS.items() if bits & b]
+    rest = bits & ~sum(ERROR_BITS)
+    return "; ".join(names + ([f"unknown bits {rest:#x}"] if rest else [])) or "none"
+
+
 def call(name, *args):
     """Call entry point `name`; raise RuntimeError with the library's message on failure."""
     lib = load()
@@ -102,6 +129,44 @@ def call(name, *args):
     if rc != 0:
         msg = lib.exkv_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
+    if _CHECK and name not in _NO_STREAM:
+        bits = stream_error_bits(args[-1], clear=True)
+        if bits:
+            raise RuntimeError(f"{name}: kernel error bits {bits:#x} ({describe_errors(bits)})")
+
+
+_hip_rt = None
+_ERRBUF = {}
+
+
+def _stream_device(st):
+    """Device index of a raw HIP stream handle (the null stream: the current device)."""
+    global _hip_rt
+    if _hip_rt is None:
+        import torch
+        _hip_rt = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+        _hip_rt.hipStreamGetDevice.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    d = ctypes.c_int(-1)
+    if _hip_rt.hipStreamGetDevice(st, ctypes.byref(d)) != 0:
+        raise RuntimeError("hipStreamGetDevice failed")
+    return d.value
+
+
+def stream_error_bits(st, clear=True):
+    """The library's sticky kernel error bits on the GPU of raw stream `st`, once the work
+    queued on `st` so far has completed (this waits for it); clear: reset them."""
+    import torch
+    dev = _stream_device(st)
+    buf = _ERRBUF.get(dev)
+    if buf is None:
+        buf = _ERRBUF[dev] = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", dev))
+    lib = load()
+    if lib.exkv_error_bits(buf.data_ptr(), int(bool(clear)), st) != 0:
+        raise RuntimeError("exkv_error_bits failed: " + lib.exkv_last_error().decode(errors="replace"))
+    _hip_rt.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    if _hip_rt.hipStreamSynchronize(st) != 0:
+        raise RuntimeError("hipStreamSynchronize failed")
+    return int(buf.cpu().item()) & 0xFFFFFFFF
 
 
 _raw_stream = None

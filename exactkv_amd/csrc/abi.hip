@@ -24,7 +24,15 @@ int hip_status(hipError_t e, const char* where) {
 
 }  // namespace exkv
 
-extern "C" int exkv_abi_version(void) { return 3; }
+extern "C" int exkv_abi_version(void) { return 4; }
+
+extern "C" int exkv_error_bits(uint32_t* out, int32_t clear, hipStream_t stream) {
+    EXKV_REQUIRE(out, "error_bits: null output");
+    hipError_t e = exkv::fetch_errors_attention(out, 1, clear, stream);
+    if (e == hipSuccess) e = exkv::fetch_errors_encode(out, 0, clear, stream);
+    if (e == hipSuccess) e = exkv::fetch_errors_wire(out, 0, clear, stream);
+    return exkv::hip_status(e, "error_bits");
+}
 
 extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 

@@ -132,6 +132,7 @@ struct AttnArgs {
     int64_t bt_stride;
     int pool_pages;
     int D;                    // head dim: 128 (the tuned kernels), 64 or 256 (attn_dgen_kernel)
+    int spin;                 // bound of every wait on another wavefront's LDS flag (polls, >= 1)
 };
 
 // ---- split merge (kernels.py:33-43): M = max_s m_s, w_s = 2^(m_s - M),
@@ -320,10 +321,13 @@ __device__ inline void dma_page_raw(int lane, const PageMeta& m, uint32_t raw_st
         const bool isv = e >= nk;
         int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
         const int64_t rows = (int64_t)rawn.pick(isv);
-        idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+        bool bad;
+        idx = clamp_slot(idx, rows, bad);
         const uint64_t rb = rawp.pick(isv);
-        if (lane < 16 * n)
+        if (lane < 16 * n) {
+            if (bad) report_error(kErrRawSlot);
             dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
+        }
     }
 }
 
@@ -715,8 +719,10 @@ __device__ inline void balance_priority(int j, int other) {
 }
 
 // Flags between the wavefronts of a workgroup: LDS words, read and written as relaxed
-// atomics (the waits order the data accesses around them); every wait on one is bounded.
-constexpr int kSpinMax = 1 << 22;                  // bound of every flag wait (a correct run never reaches it)
+// atomics (the waits order the data accesses around them); every wait on one is bounded
+// (AttnArgs::spin polls; a correct run never reaches the bound) and a wait that reaches its
+// bound is reported (kErrWait) before the kernel goes on with whatever the LDS holds.
+constexpr int kSpinMax = 1 << 22;                  // the default bound
 __device__ inline int lds_flag_ld(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -784,7 +790,9 @@ __device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoo
             float M = fmaxf(-INFINITY, m_i);
             for (int ph = 1; ph < c.nphase; ++ph) {
                 const int w = ph * a.HW + wave;
-                for (int s = 0; s < kSpinMax && lds_flag_ld(&done[w]) == 0; ++s) __builtin_amdgcn_s_sleep(1);
+                int s = 0;
+                for (; s < a.spin && lds_flag_ld(&done[w]) == 0; ++s) __builtin_amdgcn_s_sleep(1);
+                if (s == a.spin) report_error(kErrWait);
                 asm volatile("" ::: "memory");
                 M = fmaxf(M, ld_ml(w, 0));
             }
@@ -832,7 +840,7 @@ __global__ void attn_split_kernel(AttnArgs a);
 // compute wavefront waits for ready[w] > j, reads the page, and hands the stage back as
 // soon as its last LDS read of it has returned. So the compute wavefronts never stall on a
 // full memory pipeline (the loaders do), and the CU's loads stay in flight while they
-// compute. The flags live in LDS; every wait on them is bounded (kSpinMax).
+// compute. The flags live in LDS; every wait on them is bounded (AttnArgs::spin).
 constexpr int kLoaders = 2;
 constexpr int kWpl = kWaves / kLoaders;          // compute wavefronts per loader
 constexpr int kCompThreads = 64 * (kWaves + kLoaders);
@@ -877,7 +885,9 @@ __device__ __forceinline__ void comp_loader(const AttnArgs& a, const SplitCoords
             if (lds_flag_ld(&avail[w]) <= j) {         // its stage is still in use: publish all, then wait
                 wait_vm<0>();
                 while (inflight > 0) publish();
-                for (int s = 0; s < kSpinMax && lds_flag_ld(&avail[w]) <= j; ++s) __builtin_amdgcn_s_sleep(1);
+                int s = 0;
+                for (; s < a.spin && lds_flag_ld(&avail[w]) <= j; ++s) __builtin_amdgcn_s_sleep(1);
+                if (s == a.spin) report_error(kErrWait);
             }
             int32_t e = 0;
             if (a.block_table != nullptr)
@@ -1005,7 +1015,9 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
             else
                 wait_vm<0>();
             if (lds_flag_ld(&ready[wave]) <= j) {      // page j's bytes: published by the loader
-                for (int s = 0; s < kSpinMax && lds_flag_ld(&ready[wave]) <= j; ++s) __builtin_amdgcn_s_sleep(0);
+                int s = 0;
+                for (; s < a.spin && lds_flag_ld(&ready[wave]) <= j; ++s) __builtin_amdgcn_s_sleep(0);
+                if (s == a.spin) report_error(kErrWait);
             }
             asm volatile("" ::: "memory");
             const uint32_t sb = ring + (uint32_t)(stg * STB);
@@ -1437,9 +1449,13 @@ __device__ inline int dgen_issue(const AttnArgs& a, const DLanes<D, COMP>& o, in
             const bool isv = e >= nk;
             int64_t idx = isv ? (int64_t)m.ov + (e - nk) : (int64_t)m.ok + e;
             const int64_t rows = isv ? a.v.raw_rows : a.k.raw_rows;
-            idx = idx < 0 ? 0 : (idx >= rows ? rows - 1 : idx);
+            bool bad;
+            idx = clamp_slot(idx, rows, bad);
             const uint8_t* rb = reinterpret_cast<const uint8_t*>(isv ? a.v.raw : a.k.raw);
-            if (lane < LPR * nr) dma16(rb + idx * (2 * D) + (lane % LPR) * 16, raw_st);
+            if (lane < LPR * nr) {
+                if (bad) report_error(kErrRawSlot);
+                dma16(rb + idx * (2 * D) + (lane % LPR) * 16, raw_st);
+            }
             ++n;
         }
     }
@@ -1818,6 +1834,9 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
 // and end (hipExtLaunchKernelGGL), consumed by that launch.
 static thread_local hipEvent_t t_split_start = nullptr, t_split_stop = nullptr;
 
+// Test hook: the bound of the split kernels' flag waits for launches on this thread.
+static thread_local int t_wait_limit = kSpinMax;
+
 template <int D>
 static void launch_dgen(bool comp, const AttnArgs& a, hipEvent_t e0, hipEvent_t e1, hipStream_t stream) {
     // one-dimensional: the kernel orders (sequence, split, head group, KV head) itself
@@ -1858,6 +1877,17 @@ extern "C" int64_t exkv_merge_counters(int32_t B, int32_t Hq, int32_t Hkv, int32
     const int64_t units = (int64_t)B * (Hkv / heads_per_block(Hkv)) * ((Hq / Hkv + 15) / 16);
     return units * (merge_groups(nsplit) + 1);
 }
+
+extern "C" int exkv_set_wait_limit(int32_t polls) {
+    t_wait_limit = polls > 0 ? polls : kSpinMax;
+    return EXKV_OK;
+}
+
+namespace exkv {
+hipError_t fetch_errors_attention(uint32_t* out, int first, int clear, hipStream_t stream) {
+    return fetch_file_errors(out, first, clear, stream);
+}
+}  // namespace exkv
 
 extern "C" int exkv_time_next_split(hipEvent_t start, hipEvent_t stop) {
     t_split_start = start;
@@ -1904,6 +1934,7 @@ static int fill_compressed(AttnArgs& a, const void* q, const void* k_sm, const v
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
     a.HW = heads_per_block(Hkv);
     a.D = D;
+    a.spin = t_wait_limit;
     return EXKV_OK;
 }
 
@@ -1923,6 +1954,7 @@ static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, f
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
     a.HW = heads_per_block(Hkv);
     a.D = D;
+    a.spin = t_wait_limit;
     return EXKV_OK;
 }
 

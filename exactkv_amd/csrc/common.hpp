@@ -113,6 +113,10 @@ __device__ inline int block_excl_scan(int v, int& total) {
 namespace exkv {
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* where);
+// Launch the fetch of one source file's sticky error word (errors.hpp) on `stream`.
+hipError_t fetch_errors_attention(uint32_t* out, int first, int clear, hipStream_t stream);
+hipError_t fetch_errors_encode(uint32_t* out, int first, int clear, hipStream_t stream);
+hipError_t fetch_errors_wire(uint32_t* out, int first, int clear, hipStream_t stream);
 }  // namespace exkv
 
 #define EXKV_OK 0

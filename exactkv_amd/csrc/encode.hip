@@ -402,7 +402,7 @@ static void launch_scan(const EncArgs& a, int64_t n, hipStream_t stream) {
 // the generation, so consecutive calls on one stream share a workspace; calls that
 // overlap on one workspace race.
 constexpr uint64_t kInclusive = 1ull << 31;
-constexpr int kLookbackSpin = 1 << 22;              // bound of the look-back's waits (never reached)
+constexpr int kLookbackSpin = 1 << 22;              // bound of the look-back's waits (never reached; reported)
 
 __device__ inline uint64_t ws_ld(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline void ws_st(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -434,6 +434,7 @@ __device__ inline int64_t chain_lookback(const uint64_t* ws, uint32_t tag, int t
             return excl + (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(st & 0x7FFFFFFFull), stop);
         t -= 64;
     }
+    if (lane == 0) report_error(kErrLookback);          // gave up: the prefix is partial
     return excl;
 }
 
@@ -457,7 +458,10 @@ __global__ void __launch_bounds__(1024) scan_chain_kernel(EncArgs a, int nunits,
     __syncthreads();
     const int tile = s_tile;
     const uint32_t tag = chain_tag(s_gen);
-    if ((uint32_t)tile >= (uint32_t)nblocks) return;   // a workspace left inconsistent (misuse): write nothing
+    if ((uint32_t)tile >= (uint32_t)nblocks) {         // a workspace left inconsistent (misuse): write nothing
+        if (threadIdx.x == 0) report_error(kErrScanWs);
+        return;
+    }
     const int u = tile * kScanUnits + threadIdx.x;
     int bi = 0, pg = 0, hk = 0;
     int64_t page = 0;
@@ -1083,3 +1087,9 @@ extern "C" int exkv_decode_to_bf16(const void* sm, const void* code, const void*
     launch_decode_any(D, a, (int64_t)B * (TS / kPage) * H, stream);
     return launch_status("decode_to_bf16");
 }
+
+namespace exkv {
+hipError_t fetch_errors_encode(uint32_t* out, int first, int clear, hipStream_t stream) {
+    return fetch_file_errors(out, first, clear, stream);
+}
+}  // namespace exkv

@@ -12,6 +12,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "errors.hpp"
 
 namespace exkv {
 
@@ -77,12 +78,22 @@ __device__ inline void rebuild_values(const PageBytes& pb, uint32_t out[16]) {
 }
 
 // Slot of token r's raw row: rowoff + popcount(rowmask & ((1 << r) - 1)) (reference
-// kernels.py:119-123), clamped to the pool so that a page whose raw rows did not fit
-// (the pool counter passed its capacity, which the host repairs by growing and
-// re-encoding) cannot read out of bounds.
+// kernels.py:119-123), clamped to the pool so that a page whose metadata is broken (say,
+// read before the host repaired an overflow) cannot read out of bounds; a clamp of a row
+// that token r really has is reported (kErrRawSlot).
+// raw_slot_checked: the same with the report as a flag (host-callable, for the CPU build's
+// test): bad is set when token r has a raw row and its slot had to be clamped.
+__host__ __device__ inline int64_t raw_slot_checked(uint32_t rmask, int32_t roff, int r, int64_t raw_rows,
+                                                    bool& bad) {
+    const int64_t slot = clamp_slot((int64_t)roff + __builtin_popcount(rmask & ((1u << r) - 1u)), raw_rows, bad);
+    bad = bad && ((rmask >> r) & 1u);
+    return slot;
+}
 __device__ inline int64_t raw_slot(uint32_t rmask, int32_t roff, int r, int64_t raw_rows) {
-    int64_t slot = (int64_t)roff + popc32(rmask & ((1u << r) - 1u));
-    return slot < 0 ? 0 : (slot >= raw_rows ? raw_rows - 1 : slot);
+    bool bad;
+    const int64_t slot = raw_slot_checked(rmask, roff, r, raw_rows, bad);
+    if (bad) report_error(kErrRawSlot);
+    return slot;
 }
 
 // The lane's 32 values of a raw row (channels 16g.. and 64+16g..).

@@ -22,6 +22,7 @@
 // Sequences whose arguments do not fit (tokens, blob size, or for unpack the blob header)
 // are skipped, so no access leaves the buffers; the Python wrappers check them first.
 #include "common.hpp"
+#include "errors.hpp"
 #include "../../include/exactkv.h"
 
 namespace exkv {
@@ -320,7 +321,9 @@ __global__ void __launch_bounds__(256) wire_copy_kernel(WireArgs a) {
                 copy_rows(m, lane,
                           [&](int k) -> const uint16_t* {
                               const int64_t br = (int64_t)first + k;
-                              const int64_t slot = min(max((int64_t)roff + k, (int64_t)0), a.raw_rows - 1);
+                              bool bad;
+                              const int64_t slot = clamp_slot((int64_t)roff + k, a.raw_rows, bad);
+                              if (bad && br < blob_rows) report_error(kErrWire);
                               return br < blob_rows ? a.raw + slot * kD : nullptr;
                           },
                           [&](int k) -> uint16_t* { return braw + ((int64_t)first + k) * kD; });
@@ -440,3 +443,9 @@ extern "C" int exkv_wire_unpack(void* sm, void* code, void* base, int32_t* rowma
     hipLaunchKernelGGL(wire_copy_kernel<true>, dim3(max_tokens / kPage + 1, nseq), dim3(256), 0, stream, a);
     return hip_status(hipGetLastError(), "wire_unpack");
 }
+
+namespace exkv {
+hipError_t fetch_errors_wire(uint32_t* out, int first, int clear, hipStream_t stream) {
+    return fetch_file_errors(out, first, clear, stream);
+}
+}  // namespace exkv

@@ -53,6 +53,28 @@ def plan_splits(B, Hkv, Hq, T, target_blocks=256, min_split=16):
     return ns.value, sl.value
 
 
+def error_bits(device=None, clear=True):
+    """The library's sticky kernel error bits on `device` (default: the current one), read
+    after the work queued on its current stream has completed: 0 when no kernel has given up
+    a bounded wait or clamped an out-of-pool index since the last clear (see
+    _lib.ERROR_BITS / include/exactkv.h EXKV_ERR_*). clear: reset them."""
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    return _lib.stream_error_bits(_lib.stream(idx), clear=clear)
+
+
+def check_errors(device=None):
+    """Raise RuntimeError if a kernel has set an error bit on `device` (and clear them)."""
+    bits = error_bits(device, clear=True)
+    if bits:
+        raise RuntimeError(f"exactkv kernel error bits {bits:#x}: {_lib.describe_errors(bits)}")
+
+
+def set_wait_limit(polls):
+    """Test hook: bound the split kernels' inter-wavefront flag waits of this thread's later
+    attention calls to `polls` polls (<= 0: the default, never reached by a correct call)."""
+    _lib.call("exkv_set_wait_limit", int(polls))
+
+
 _WS = {}  # split partials, reused per (device, stream, rows, nsplit): kernels on one stream run in order
 _CNT = {}  # merge arrival counters per (device, stream, units): zero between calls
 

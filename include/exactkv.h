@@ -34,8 +34,37 @@ extern "C" {
 typedef struct ihipStream_t* hipStream_t;
 
 /* ABI version of the library (2: the encoders take a scan workspace; 3: head dims 64 and
- * 256 and exkv_plan_splits_hd). */
+ * 256 and exkv_plan_splits_hd; 4: exkv_error_bits and exkv_set_wait_limit). */
 int exkv_abi_version(void);
+
+/* Sticky error bits of the kernels. A kernel that gives up a bounded wait (a correct call
+ * never reaches the bound) or clamps an index that a broken invariant put out of bounds
+ * (say, attention over a page whose raw rows overflowed the pool before check_overflow
+ * repaired it) carries on -- no access leaves its buffers -- but its results are then not
+ * the format's bits although the call returned 0; it records that by OR-ing a bit into
+ * an error word that the library keeps on the GPU (one per kernel source file, zero when
+ * the library loads). */
+#define EXKV_ERR_WAIT 0x1u      /* attention: a wait on another wavefront's LDS flag gave up */
+#define EXKV_ERR_RAW_SLOT 0x2u  /* attention, decode: a raw row's pool slot lay outside the pool */
+#define EXKV_ERR_LOOKBACK 0x4u  /* encoder: the slot scan's look-back gave up on a predecessor */
+#define EXKV_ERR_SCAN_WS 0x8u   /* encoder: an inconsistent scan workspace (more blocks than tickets) */
+#define EXKV_ERR_WIRE 0x10u     /* wire pack: a raw row's pool slot lay outside the pool */
+
+/* out (a device uint32 on the GPU of `stream`) = the OR of the error words of that GPU, in
+ * stream order (three small kernels; nothing synchronizes, nothing is allocated); clear != 0
+ * resets the words. Bits set by kernels on other streams of the GPU are included once they
+ * have completed.
+ * No counterpart in the reference, whose one such condition, raw-pool overflow, is a
+ * counter the host reads (cache.py:149-158); that protocol is unchanged here. */
+int exkv_error_bits(uint32_t* out, int32_t clear, hipStream_t stream);
+
+/* Test hook: the bound, in polls, of every wait of the split kernels on another wavefront's
+ * LDS flag, for the attention calls the calling thread makes afterwards (<= 0: the default,
+ * 2^22 polls, which a correct call never reaches). A tiny bound makes those waits give up
+ * (the call then returns garbage and sets EXKV_ERR_WAIT; every access stays in bounds and
+ * the kernel ends normally), so a test can check that a give-up is reported.
+ * No counterpart in the reference. */
+int exkv_set_wait_limit(int32_t polls);
 
 /* Message of the last failed call on this thread. */
 const char* exkv_last_error(void);

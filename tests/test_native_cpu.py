@@ -129,3 +129,31 @@ def test_engine_module_imports_without_a_gpu():
     from exactkv_amd import engine
     assert exactkv.Engine is engine.Engine
     assert set(engine.BACKENDS) == {"exactkv", "bf16"}
+
+
+def test_clamp_detection_of_the_error_bits(tmp_path):
+    """The raw-slot clamp behind EXKV_ERR_RAW_SLOT, built for the host: the slot is always
+    inside the pool, unchanged when it already was, and flagged exactly for a token whose raw
+    row had to be clamped (tests/native/errors_check.cpp)."""
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "errors_check"
+    subprocess.run([hipcc, "-O2", "-o", str(exe), os.path.join(ROOT, "tests", "native", "errors_check.cpp")],
+                   check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
+    assert r.returncode == 0, r.stdout
+    assert " 0 failures" in r.stdout
+
+
+def test_error_bits_are_declared_and_described():
+    """Every EXKV_ERR_* bit of the header has a description on the Python side, and the
+    description of a word names each of its bits (and unknown ones)."""
+    import re
+    from exactkv_amd import _lib
+    hdr = open(os.path.join(ROOT, "include", "exactkv.h")).read()
+    bits = {int(v, 16) for v in re.findall(r"#define EXKV_ERR_\w+ (0x[0-9a-fA-F]+)u", hdr)}
+    assert bits == set(_lib.ERROR_BITS)
+    assert _lib.describe_errors(0) == "none"
+    d = _lib.describe_errors(0x1 | 0x4 | 0x100)
+    assert _lib.ERROR_BITS[0x1] in d and _lib.ERROR_BITS[0x4] in d and "0x100" in d

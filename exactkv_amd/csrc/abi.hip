@@ -37,7 +37,7 @@ extern "C" int exkv_error_bits(uint32_t* out, int32_t clear, hipStream_t stream)
 extern "C" const char* exkv_last_error(void) { return exkv::g_err; }
 
 // Split plan for MI355X: about target_blocks workgroups in total over B * (Hkv / HW) * head
-// groups, where a workgroup covers HW = gcd(Hkv, 8) KV heads -- 256 by default, one per
+// groups, where a workgroup covers HW = min(gcd(Hkv, 8), 4) KV heads -- 256 by default, one per
 // CU, since a workgroup holds ~150 KB of LDS -- with
 // at least min_split tokens per split (16 by default, one page: a wavefront's pages follow
 // one another at about one memory round trip each, so a few units are served best by many
@@ -87,12 +87,13 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
     if (target_blocks <= 0) target_blocks = 256;
     if (min_split <= 0) min_split = exkv::kPage;
     const int64_t hg = (Hq / Hkv + 15) / 16;
-    int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8)
+    int hw = Hkv, m = 8;                               // KV heads per workgroup: gcd(Hkv, 8), at most 4
     while (m) {
         const int t = hw % m;
         hw = m;
         m = t;
     }
+    if (hw > 4) hw = 4;
     plan_core((int64_t)B * (Hkv / hw) * hg, T, target_blocks, min_split, nsplit, split_len);
     return EXKV_OK;
 }

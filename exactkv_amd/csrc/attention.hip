@@ -3,9 +3,9 @@
 // Reference: exactkv/kernels.py _split_c_kernel :142-165, _split_ref_kernel :168-194,
 // _attn_block :46-59, _reduce_kernel :33-43.
 //
-// Grid: x = token split, y = (sequence, block of gcd(Hkv, 8) KV heads, group of 16 query
-// heads); one workgroup per CU (its LDS ring, ~158 KB). A workgroup has 8 compute
-// wavefronts: each KV head of the block gets 8 / gcd(Hkv, 8) of them ("page phases"),
+// Grid: x = token split, y = (sequence, block of HW = min(gcd(Hkv, 8), 4) KV heads, group of
+// 16 query heads); one workgroup per CU (its LDS ring, ~158 KB). A workgroup has 8 compute
+// wavefronts: each KV head of the block gets 8 / HW of them ("page phases"),
 // which take the split's 16-token pages round robin, each with its own online-softmax
 // state, and are merged through LDS at the end (one partial per split and query head).
 //
@@ -121,7 +121,7 @@ struct AttnArgs {
     int64_t lens_stride;
     int B, Hq, Hkv, G, HG, TS, T, nsplit, split_len;
     int window;               // > 0: attend to the last `window` tokens of each sequence only
-    int HW;                   // KV heads per workgroup (gcd(Hkv, 8)); 8 / HW page phases per head
+    int HW;                   // KV heads per workgroup (min(gcd(Hkv, 8), 4)); 8 / HW page phases per head
     float qk_scale;
     uint16_t* out;            // [B, Hq, 128] bf16, written by the last workgroup of each unit
     int32_t* counters;        // [gridDim.y] arrival counters (zero between calls); nullptr: no merge
@@ -595,7 +595,7 @@ __device__ inline SplitCoords split_coords(const AttnArgs& a) {
     const int nhb = a.Hkv / a.HW;
     c.hb = y % nhb;
     c.b = y / nhb;
-    c.hw_sh = __builtin_ctz(a.HW);                    // HW = gcd(Hkv, 8), a power of two
+    c.hw_sh = __builtin_ctz(a.HW);                    // HW: a power of two
     c.nphase = kWaves >> c.hw_sh;
     int len = a.lens ? a.lens[c.b * a.lens_stride] : a.T;
     len = min(max(len, 0), a.TS);
@@ -749,6 +749,22 @@ __device__ inline void store_partial(const AttnArgs& a, int64_t prow, int g, con
     }
 }
 
+// One split per row: the output itself, with the merge's arithmetic for a single term
+// (w = 2^(m - m), n = fma(o, w, 0), d = fma(l, w, 0), out = n / d; merge_direct at ns = 1),
+// so the bits are those of the separate merge and no second launch is needed.
+__device__ inline void store_direct(const AttnArgs& a, int64_t orow, int g, const f32x4 (&o)[8], float m, float l) {
+    const float w = fast_exp2(m - m);
+    const float den = __builtin_fmaf(l, w, 0.f);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        float n[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) n[k] = __builtin_fmaf(o[nb][k], w, 0.f);
+        *reinterpret_cast<uint2*>(a.out + orow * kD + 16 * nb + 4 * g) =
+            make_uint2(pack_bf16x2(n[0] / den, n[1] / den), pack_bf16x2(n[2] / den, n[3] / den));
+    }
+}
+
 // After the page loop: one partial per (split, query head). With page phases (fewer than 8
 // KV heads per workgroup), the wavefront of phase p > 0 leaves its (o, m, l) in its own
 // ring -- free once its pages are consumed: o as [16 heads][kMoRow] floats (rows padded so
@@ -783,10 +799,9 @@ __device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoo
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         lds_flag_st(&done[wave], 1);
     } else if (active && r < c.gh) {
-        const int64_t prow = ((int64_t)c.b * a.Hq + (int64_t)hk * a.G + c.hg * 16 + r) * a.nsplit + c.split;
-        if (c.nphase == 1) {                           // one wavefront per head: its own partial
-            store_partial(a, prow, g, acc, m_i, l_t);
-        } else {
+        const int64_t orow = (int64_t)c.b * a.Hq + (int64_t)hk * a.G + c.hg * 16 + r;
+        const int64_t prow = orow * a.nsplit + c.split;
+        {
             float M = fmaxf(-INFINITY, m_i);
             for (int ph = 1; ph < c.nphase; ++ph) {
                 const int w = ph * a.HW + wave;
@@ -820,10 +835,13 @@ __device__ __forceinline__ void split_epilogue(const AttnArgs& a, const SplitCoo
                     l += wp * ld_ml(w, 1);
                 }
             }
-            store_partial(a, prow, g, o, M, l);
+            if (a.nsplit == 1 && a.out != nullptr)
+                store_direct(a, orow, g, o, M, l);
+            else
+                store_partial(a, prow, g, o, M, l);
         }
     }
-    merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
+    if (a.nsplit > 1) merge_tail(a, c.b, c.hb, c.hg, c.gh, c.split);
 }
 
 template <bool COMP>
@@ -1789,7 +1807,12 @@ __global__ void __launch_bounds__(64) attn_reduce_d_kernel(const float* po, cons
 
 using namespace exkv;
 
-// KV heads per workgroup: gcd(Hkv, 8) (8 wavefronts = head slots x page phases)
+// KV heads per workgroup: gcd(Hkv, 8), at most 4 (8 wavefronts = head slots x page phases,
+// so every head gets at least two phases). At 8 KV heads four per workgroup halves the
+// partials a call merges and is never slower: measured (split kernel / call, 8 against 4
+// heads per workgroup) c2a 40.5 / 44.7 against 40.5 / 44.2 us, c2a with a partial last
+// page 41.8 / 46.0 against 41.7 / 45.3, B1 x 128K 77.3 / 79.8 against 75.6 / 79.0, B32 x
+// 4096 77.6 / 79.7 against 77-80 / 79-80, B128 x 4352 302.8 / 307.9 against 301.6 / 305.8.
 static int heads_per_block(int Hkv) {
     int a = Hkv, b = kWaves;
     while (b) {
@@ -1797,7 +1820,7 @@ static int heads_per_block(int Hkv) {
         a = b;
         b = t;
     }
-    return a;
+    return a < 4 ? a : 4;
 }
 
 static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_t* lens, int nsplit,
@@ -1977,9 +2000,10 @@ extern "C" int exkv_attn_compressed(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, E
     int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {   // merge fused into the split kernel (D = 128)
+    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+        // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
-        a.counters = ws_cnt;
+        a.counters = nsplit > 1 ? ws_cnt : nullptr;
         return launch_split(true, a, stream);
     }
     rc = launch_split(true, a, stream);
@@ -1998,9 +2022,10 @@ extern "C" int exkv_attn_bf16(const void* q, const void* k, const void* v, float
     int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
+    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+        // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
-        a.counters = ws_cnt;
+        a.counters = nsplit > 1 ? ws_cnt : nullptr;
         return launch_split(false, a, stream);
     }
     rc = launch_split(false, a, stream);
@@ -2037,9 +2062,10 @@ extern "C" int exkv_attn_compressed_paged(EXKV_C_PARAMS, int32_t* ws_cnt, void* 
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed_paged: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
+    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+        // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
-        a.counters = ws_cnt;
+        a.counters = nsplit > 1 ? ws_cnt : nullptr;
         return launch_split(true, a, stream);
     }
     rc = launch_split(true, a, stream);
@@ -2062,9 +2088,10 @@ extern "C" int exkv_attn_bf16_paged(const void* q, const void* k, const void* v,
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16_paged: null output");
-    if (ws_cnt && nsplit <= kFusedMaxSplits && D == kD) {
+    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+        // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
-        a.counters = ws_cnt;
+        a.counters = nsplit > 1 ? ws_cnt : nullptr;
         return launch_split(false, a, stream);
     }
     rc = launch_split(false, a, stream);

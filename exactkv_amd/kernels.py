@@ -90,9 +90,9 @@ def _workspace(dev, rows, ns, D, st=None):
 
 
 def merge_units(B, Hkv, Hq):
-    """Workgroup units of the split kernel: sequences x KV-head blocks of gcd(Hkv, 8) x
-    groups of 16 query heads per KV head."""
-    return B * (Hkv // math.gcd(Hkv, 8)) * (-(-(Hq // Hkv) // 16))
+    """Workgroup units of the split kernel: sequences x KV-head blocks of min(gcd(Hkv, 8), 4)
+    x groups of 16 query heads per KV head."""
+    return B * (Hkv // min(math.gcd(Hkv, 8), 4)) * (-(-(Hq // Hkv) // 16))
 
 
 FUSED_MERGE_MAX_SPLITS = 1024   # up to this many splits the split kernel can merge in its tail

@@ -51,8 +51,8 @@ def _ref_case(B, T, Hq, Hkv, seed):
     return q, k, v
 
 
-# KV heads per workgroup gcd(Hkv, 8) = 4, 8, 8, 2, 2, 1, 1, 2: every page-phase count (1,
-# 2, 4, 8), so each loader wavefront serves wavefronts of one phase or of several
+# KV heads per workgroup min(gcd(Hkv, 8), 4) = 4, 4, 4, 2, 2, 1, 1, 2: every page-phase
+# count (2, 4, 8), so each loader wavefront serves wavefronts of one phase or of several
 SHAPES = [(1, 4096, 28, 4), (3, 1000, 32, 8), (2, 333, 32, 32), (4, 17, 16, 2), (2, 500, 64, 2), (1, 1, 8, 1),
           (2, 700, 8, 1), (2, 777, 12, 6)]
 
@@ -114,7 +114,7 @@ def test_default_plans_of_small_grids(B, Hq, Hkv, T):
     kc, vc = _encode(kd), _encode(vd)
     ns, sl = kernels.plan_splits(B, Hkv, Hq, T)
     _say("default plan", B, Hq, Hkv, T, ns, sl)
-    assert sl <= 32
+    assert sl <= 64                   # one round of ~256 workgroups over at most 2 units
     o_c = kernels.attention_compressed(qd, kc, vc, T)
     o_r = kernels.attention_reference(qd, kd, vd, T)
     assert same_bits(o_c, o_r)
@@ -273,3 +273,34 @@ def test_merge_kernel_against_oracle(ns):
     ref = oatt.merge_splits(m, l, o)
     got = out.float().cpu().numpy()
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,window", [(3, 1000, 32, 8, 0), (2, 777, 28, 4, 0), (4, 300, 16, 2, 100),
+                                               (1, 2048, 8, 1, 0)])
+def test_one_split_writes_the_merge_bits(B, T, Hq, Hkv, window):
+    """With one split the split kernel writes the output itself (no merge launch). Its bits
+    must be those of the split kernel's partials merged by the separate merge kernel, in the
+    compressed kernel and in the twin, contiguous and paged."""
+    from exactkv_amd import _lib
+    q, k, v = _ref_case(B, T, Hq, Hkv, seed=930 + T)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    TS = kc.TS
+    _say("one split", B, T, Hq, Hkv, window)
+    direct = kernels.attention_compressed(qd, kc, vc, T, nsplit=1, split_len=TS, window=window)
+    twin = kernels.attention_reference(qd, kd, vd, T, nsplit=1, split_len=TS, window=window)
+    assert same_bits(direct, twin)
+    # the two-launch form: the split kernel into a workspace, then exkv_attn_reduce
+    wo = torch.empty(B * Hq, 1, 128, dtype=torch.float32, device=DEV)
+    wm, wl = (torch.empty(B * Hq, 1, dtype=torch.float32, device=DEV) for _ in range(2))
+    ka, _, _, _ = kernels._cache_args(kc)
+    va, _, _, _ = kernels._cache_args(vc)
+    _lib.call("exkv_attn_split_compressed", qd.data_ptr(), *ka, *va, wo.data_ptr(), wm.data_ptr(), wl.data_ptr(),
+              B, Hq, Hkv, 128, T, TS, None, 0, 1, TS, window, 128 ** -0.5 * kernels.LOG2E, _lib.stream())
+    out = torch.empty_like(qd)
+    _lib.call("exkv_attn_reduce", _lib.ptr(wo), _lib.ptr(wm), _lib.ptr(wl), _lib.ptr(out), B * Hq, 1, 128,
+              _lib.stream())
+    assert same_bits(direct, out)
+    lo = T - window if window else 0
+    ref = oatt.attention(u16(q), u16(k[:, lo:T]), u16(v[:, lo:T]), T - lo, np.float32)
+    assert_bf16_tolerance(direct, ref)

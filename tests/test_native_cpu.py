@@ -74,17 +74,17 @@ def test_argument_errors_are_reported_without_launching():
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,expect", [
-    (8, 8, 32, 8192, (32, 256)),       # a workgroup covers all 8 KV heads: 8 units x 32 splits = 256
-    (1, 8, 32, 131072, (256, 512)),
+    (8, 8, 32, 8192, (16, 512)),       # a workgroup covers 4 of the 8 KV heads: 16 units x 16 splits = 256
+    (1, 8, 32, 131072, (128, 1024)),
     (1, 4, 28, 32768, (256, 128)),     # 4 KV heads per workgroup: one unit, 256 splits
-    (32, 8, 32, 4096, (8, 512)),
+    (32, 8, 32, 4096, (4, 1024)),
     (1, 4, 28, 8000, (250, 32)),       # one unit: 256 splits of at least a page, rounded to 32 tokens
     (4, 2, 16, 17, (2, 16)),           # capped by one page per split
     (2, 2, 64, 1000, (63, 16)),        # G = 32: two head groups per KV head, 4 units; one page per split
-    (620, 8, 32, 4352, (2, 2176)),     # more units than one round: >= 2 rounds, the last >= 95% full (4.84 rounds)
-    (256, 8, 32, 4096, (2, 2048)),     # exactly two rounds
-    (300, 8, 32, 4096, (5, 832)),      # 5.86 rounds: the first split count whose last round is >= 95% full
-    (255, 8, 32, 4096, (2, 2048)),     # still one round of units: two splits reach 256 blocks
+    (620, 8, 32, 4352, (1, 4352)),     # 1240 units, more than a round: one split gives 4.84 rounds, the last 97% full
+    (256, 8, 32, 4096, (1, 4096)),     # 512 units: exactly two rounds
+    (300, 8, 32, 4096, (5, 832)),      # 600 units, 11.7 rounds: the first split count whose last round is >= 95% full
+    (255, 8, 32, 4096, (2, 2048)),     # 510 units: one split would give 1.99 rounds, two give 3.98
 ])
 def test_plan_splits(B, Hkv, Hq, T, expect):
     from exactkv_amd.kernels import plan_splits
@@ -100,7 +100,7 @@ def test_plan_splits(B, Hkv, Hq, T, expect):
     (1, 8, 32, 131072, 256, (64, 2048)),
     (2, 2, 64, 1000, 64, (16, 64)),      # G = 32: two head groups per KV head, 8 units; capped by 64-token splits
     (600, 8, 32, 4096, 64, (2, 2048)),   # 4800 units, 9.4 rounds: two splits fill the last round to 98.7%
-    (8, 8, 32, 8192, 128, (32, 256)),    # head dim 128: exkv_plan_splits
+    (8, 8, 32, 8192, 128, (16, 512)),    # head dim 128: exkv_plan_splits
 ])
 def test_plan_splits_hd(B, Hkv, Hq, T, D, expect):
     from exactkv_amd.kernels import plan_splits, plan_splits_hd

@@ -225,6 +225,18 @@ def time_graph(fn, n, warmup, copies, per_graph=32):
     return e0.elapsed_time(e1) / (reps * per_graph)
 
 
+def graph_cost_split(fn, warmup, copies, small=32, large=128, reps=8):
+    """Graph replay time t(n) of graphs of n calls = F + n * c: the marginal cost c of a call
+    inside a graph and the fixed cost F of launching one graph, from graphs of `small` and
+    `large` calls (each replayed `reps` times back to back, HIP events on the launch stream).
+    graph_replay_us (graphs of 32 calls) is c + F / 32."""
+    t_small = time_graph(fn, small * reps, warmup, copies, per_graph=small)
+    t_large = time_graph(fn, large * reps, warmup, copies, per_graph=large)
+    c = (large * t_large - small * t_small) / (large - small)
+    return {"per_call_us": round(c * 1e3, 2), "per_graph_launch_us": round((t_small - c) * small * 1e3, 1),
+            "calls_per_graph": [small, large]}
+
+
 def cpu_threads():
     """Host threads for the CPU baseline: every core this process may run on."""
     return len(os.sched_getaffinity(0))
@@ -388,6 +400,7 @@ def main():
     ms_split_b, _ = time_split_kernel(lambda i: split_only(kernels, q, kbs[i], vbs[i], T, ns, sl, False, window=W),
                                       max(a.steps, 50), a.warmup, a.copies)
     ms_c_graph = time_graph(full_c, max(a.steps, 200), a.warmup, a.copies)
+    graph_split = graph_cost_split(full_c, a.warmup, a.copies)
     med, p10, p90 = time_calls(full_c, max(a.steps, 50), a.warmup, a.copies)
     print("[bench] attention timed", file=sys.stderr, flush=True)
 
@@ -416,6 +429,7 @@ def main():
         "settle_calls": settled,
         "graph_replay_us": round(ms_c_graph * 1e3, 2),
         "graph_replay_calls": max(a.steps, 200),
+        "graph_replay_split": graph_split,
         "per_call_us": {"median": round(med * 1e3, 2), "p10": round(p10 * 1e3, 2), "p90": round(p90 * 1e3, 2),
                         "calls": max(a.steps, 50)},
         "bf16_twin_us": round(ms_b * 1e3, 2),

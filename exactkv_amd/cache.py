@@ -5,16 +5,17 @@ append(x), T, nbytes(), buffers(), check_overflow(caches).
 How CompressedKV is organised here:
 
 * Six device arrays per cache in the codec's layout (sm, code, base, rowmask, rowoff, raw)
-  plus three int32 words on the device: the raw-row counter `cnt`, its value before the
-  latest page encode, and `state[0]`, the number of tokens held.
+  plus int32 words on the device: the raw-row counter `cnt`, its value before the latest
+  page encode, and `state[0]`, the number of tokens held (`state[1]` is the append
+  kernel's arrival counter, zero between calls).
 * The raw array is two regions. Rows [0, cap) take escaped rows in the codec's order
   (sequence, page, head, token), which keeps every byte equal to codec.encode's. Behind
   them each (sequence, head) owns 16 rows holding its open page -- the newest, partly
   filled one -- as bf16; that page is marked all-raw, so the attention and decode kernels
   read it through rowmask / rowoff like any escaped row.
 * Everything a decode step changes is computed on the device from `state[0]`: the append
-  kernels write the token into the open page, encode the page when it fills, open the next
-  one and advance the count; exkv_cache_open_page re-derives the open page's rowmask /
+  kernel (one launch) writes the token into the open page, encodes the page when it fills,
+  places its raw rows, opens the next page and advances the count; exkv_cache_open_page re-derives the open page's rowmask /
   rowoff after a prefill or a pool move. No host value enters a step, so a step can be
   captured once and replayed.
 * The host keeps a mirror `T` of the token count for its checks, and runs the overflow
@@ -161,8 +162,8 @@ class CompressedKV:
             raise ValueError(f"append expects a bf16 [{self.B}, {self.H}, {self.D}] tensor with contiguous rows")
 
     def _launch_append(self, x):
-        """Tail write (+ page encode and next page opened at a page end), slot scan, raw-row
-        copy: three kernels that read the token count from state[0]."""
+        """Tail write (+ at a page end: page encode, slot scan, raw-row copy, next page
+        opened): one kernel that reads the token count from state[0] and advances it."""
         _lib.call("exkv_cache_append", _lib.ptr(x, align=2, what="x"), x.stride(0), x.stride(1),
                   _lib.ptr(self.sm), _lib.ptr(self.code), _lib.ptr(self.base), _lib.ptr(self.rowmask),
                   _lib.ptr(self.rowoff), _lib.ptr(self.raw), _lib.ptr(self.cnt, 4), _lib.ptr(self._before, 4),

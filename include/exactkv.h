@@ -104,7 +104,8 @@ int exkv_encode_pages_paged(const void* src, int64_t s_b, int64_t s_pg, int64_t 
  * whose token count is state[0] (device): write it into the tail area; when it completes
  * page T/16, encode that page (slots as above, *before = counter before) and open the next
  * page (rowmask 0xFFFF, rowoff into the tail area); then state[0] += 1. Nothing is written
- * once state[0] == TS.
+ * once state[0] == TS. One launch: state[1] is its arrival counter (zero before the first
+ * call; each call leaves it zero), so state points to at least two words.
  * Replaces: cache.py:100-112 CompressedKV.append (tail write + _encode + _open_tail). */
 int exkv_cache_append(const void* x, int64_t sx_b, int64_t sx_h, void* sm, void* code, void* base,
                       int32_t* rowmask, int32_t* rowoff, void* raw, int32_t* cnt, int32_t* before,

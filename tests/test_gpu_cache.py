@@ -81,3 +81,35 @@ def test_prefill_overflow_regrows_and_matches_codec():
     for k in ("sm", "code", "base", "rowmask", "rowoff"):
         assert np.array_equal(getattr(c, k).cpu().numpy(), ref[k]), k
     assert np.array_equal(u16(c.raw[:n]), ref["raw"])
+
+
+@pytest.mark.parametrize("B,H,T0,TS,rate", [(600, 8, 13, 48, 0.5), (1040, 8, 9, 48, 0.05)])
+def test_append_page_ends_with_many_units_and_raw_rows(B, H, T0, TS, rate):
+    """The one-launch append's page end with many (sequence, head) units: 4,800 units with
+    half the rows raw (the raw rows, several per thread of the last workgroup, found through
+    its LDS table of ranks), and 8,320 units, more than that table holds (each thread moves
+    its own units' rows). Byte-equal to the CPU model of the protocol at every page end; the
+    arrival counter state[1] is zero after every append."""
+    g = torch.Generator().manual_seed(5)
+    D = 128
+    _say("append many units", B, H, T0, TS, rate)
+    c = exactkv.CompressedKV(B, TS, H, D, reserve=0.6)
+    m = ocache.CacheModel(B, TS, H, D, reserve=0.6)
+    x0 = _make(g, B, T0, H, D, rate)
+    x0d = x0.to(DEV)
+    for b in range(B):
+        c.prefill_slot(b, x0d[b:b + 1].contiguous())
+        m.prefill_slot(b, u16(x0[b]))
+    xs = _make(g, B, TS - T0, H, D, rate)
+    xsd = xs.to(DEV)
+    ends = 0
+    for t in range(TS - T0):
+        c.append(xsd[:, t].contiguous())
+        m.append(u16(xs[:, t]))
+        exactkv.check_overflow([c])
+        m.check_overflow()
+        assert int(c.state[1].item()) == 0, t
+        if c.T % 16 == 0:
+            _state_equal(c, m, t)
+            ends += 1
+    assert ends >= 2

@@ -99,10 +99,11 @@ FUSED_MERGE_MAX_SPLITS = 1024   # up to this many splits the split kernel can me
 # With fused_merge the split kernel's last workgroups merge the partials (two levels of
 # about sqrt(nsplit) splits each; one level up to 8 splits, with the separate merge's
 # bits), writing them with device-scope stores so that no L2 write-back is needed.
-# It is not the default: measured on MI355X under graph replay it costs more than the
-# separate merge launch (c2a 62.6 vs 47.1 us per call, c2b 101.7 vs 85.1, c1 41.7 vs 27.9):
-# every workgroup waits for its stores and an arrival atomic before it can retire, which
-# delays the workgroups queued behind it, while the separate merge adds 1.5 us at c2a.
+# It is not the default: measured on MI355X it costs more than the separate merge launch
+# (eager calls: c2a 53.8 vs 44.6 us, c1 38.4 vs 19.8): every workgroup waits for its
+# stores and an arrival atomic before it can retire, and the last one of a unit then
+# loads and merges the partials, round trips that the separate launch spreads over many
+# workgroups.
 
 
 def release_workspaces():

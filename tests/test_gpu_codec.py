@@ -172,22 +172,34 @@ def test_encoder_slot_scan_full_size(B, T, H, chained):
 def test_encoder_chained_equals_multi_launch():
     """Encodes of different sizes one after another on one stream (the chained scan's
     workspace is shared: its generation advances between calls), each byte-identical to
-    the three-launch scan on the same input and counter, including
-    a raw pool too small for every raw row (slots past cap skipped, counter past cap)."""
-    cases = [(2, 64, 8, 0.05, 0.5), (4, 4096, 8, 0.02, 0.5), (1, 32, 2, 0.3, 0.5), (3, 1024, 16, 0.05, 0.002),
-             (2, 512, 8, 0.05, 0.5)]
-    for i, (B, T, H, rate, reserve) in enumerate(cases):
-        x = synthetic.make_kv(B, T, H, kind="k", seed=40 + i, raw_row_rate=rate, device=DEV)
+    the three-launch scan on the same input and counter, including a raw pool too small for
+    every raw row (slots past cap skipped, counter past cap), head dims 64 and 256, a unit
+    with every row raw, and source rows 4-byte but not 16-byte aligned (the raw-row copy's
+    word path)."""
+    cases = [(2, 64, 8, 0.05, 0.5, 128), (4, 4096, 8, 0.02, 0.5, 128), (1, 32, 2, 0.3, 0.5, 128),
+             (3, 1024, 16, 0.05, 0.002, 128), (2, 512, 8, 0.05, 0.5, 128), (4, 2048, 8, 0.05, 0.5, 64),
+             (2, 1024, 4, 0.05, 0.5, 256), (64, 512, 8, 0.01, 0.5, 128)]
+    for i, (B, T, H, rate, reserve, D) in enumerate(cases):
+        x = synthetic.make_kv(B, T, H, D=D, kind="k", seed=40 + i, raw_row_rate=rate, device=DEV)
+        if i == 2:
+            x[0, 16:32, 1] *= 2.0 ** 100                   # a floor >= 128 in every channel: all 16 rows raw
+        if i == 4:                                         # rows 4-byte aligned but not 16
+            xx = torch.empty(B, T, H, D + 2, dtype=x.dtype, device=DEV)
+            xx[..., 2:] = x
+            x = xx[..., 2:]
         st = (x.stride(0), 16 * x.stride(1), x.stride(1), x.stride(2))
         out = []
         for chained in (True, False):
-            c = exactkv.CompressedKV(B, T, H, 128, reserve=reserve)
+            c = exactkv.CompressedKV(B, T, H, D, reserve=reserve)
             c.cnt.fill_(3)
             kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // 16, chained=chained)
             out.append(c)
         a, b = out
-        _say("chained vs three-launch scan", B, T, H, "counter", int(a.cnt.item()), "cap", a.cap)
+        _say("chained vs three-launch scan", B, T, H, D, "counter", int(a.cnt.item()), "cap", a.cap)
         for f in ("sm", "code", "base", "rowmask", "rowoff", "cnt", "_before"):
             assert torch.equal(getattr(a, f), getattr(b, f)), f
         n = min(int(a.cnt.item()), a.cap)
         assert torch.equal(a.raw[:n], b.raw[:n])
+        if i == 2:
+            assert int(b.rowmask[0, 1, 1].item()) == 0xFFFF
+            assert same_bits(kernels.decode_to_bf16(b.buffers(), T), x)

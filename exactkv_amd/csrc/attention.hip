@@ -462,22 +462,34 @@ __device__ inline void write_v_tile(uint32_t sb, const LdsLane& o, int toff, con
 // invalidate (a device-scope release / acquire, which on a multi-XCD part writes back the
 // XCD's whole L2: measured slower than a second kernel at every grid size).
 //
-// Two levels keep each merge short: the splits of a unit form groups of merge_group(ns)
-// consecutive splits; the last workgroup to finish a group merges it into the group's first
-// split slot (un-normalised o, max m, sum l), and the last group merger of the unit merges
-// the groups into the output. Counters: [unit][group] then [unit][ngroups] for the second
-// level, all zero between calls (each merger resets the one it consumed).
+// Up to 32 splits the last workgroup of a unit merges them all (one level: the separate
+// merge's arithmetic, so its bits). More splits take two levels, each short: the splits of
+// a unit form groups of merge_group(ns) consecutive splits; the last workgroup to finish a
+// group merges it into the group's first split slot (un-normalised o, max m, sum l), and
+// the last group merger of the unit merges the groups into the output. Counters:
+// [unit][group] then [unit][ngroups] for the second level, all zero between calls (each
+// merger resets the one it consumed). Partial values move as 8-byte device-scope
+// atomics (a channel pair per access).
 __device__ inline void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline float ld_dev(const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ inline void st_dev4(float* p, const f32x4& v) {
-    st_dev(p, v[0]);
-    st_dev(p + 1, v[1]);
-    st_dev(p + 2, v[2]);
-    st_dev(p + 3, v[3]);
+__device__ inline void st_dev2(float* p, float x, float y) {       // p 8-byte aligned
+    const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float2 ld_dev2(const float* p) {
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+// 16 bytes with the device-scope stores' cache policy (sc1: through the writer's L2 to
+// memory), in one access: HIP has no 16-byte atomic store, and two 8-byte ones from lanes
+// holding every other channel pair would each fill only half of every 64-byte sector.
+// Completion is waited for with the other stores (arrive_last's s_waitcnt vmcnt(0)).
+__device__ inline void st_dev4(float* p, const f32x4& v) {    // p 16-byte aligned
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 
 __host__ __device__ inline int merge_group(int ns) {
-    if (ns <= 8) return ns;                            // one level (the separate merge's bits)
+    if (ns <= 32) return ns;                           // one level (the separate merge's bits)
     int g = 1;
     while (g * g < ns) ++g;                            // ceil(sqrt(ns)): both levels about as long
     return g;
@@ -500,9 +512,9 @@ __device__ inline RowMerge merge_row_dev(const AttnArgs& a, int64_t row, int s0,
 #pragma unroll
     for (int i = 0; i < 32; ++i)
         if (i < n) {
-            const float* p = po + (int64_t)(s0 + i * step) * kD + 2 * lane;
-            ox[i] = ld_dev(p);
-            oy[i] = ld_dev(p + 1);
+            const float2 v = ld_dev2(po + (int64_t)(s0 + i * step) * kD + 2 * lane);
+            ox[i] = v.x;
+            oy[i] = v.y;
         }
     const float M = wave_max(mv);
     const float ws = M == -INFINITY ? 0.f : fast_exp2(mv - M);
@@ -550,9 +562,7 @@ __device__ inline void merge_tail(const AttnArgs& a, int b, int hb, int hg, int 
         for (int i = threadIdx.x >> 6; i < rows; i += blockDim.x >> 6) {
             const int64_t row = row_of(i);
             const RowMerge r = merge_row_dev(a, row, g0, 1, gn, lane);
-            float* po = a.part_o + (row * a.nsplit + g0) * kD + 2 * lane;
-            st_dev(po, r.n0);
-            st_dev(po + 1, r.n1);
+            st_dev2(a.part_o + (row * a.nsplit + g0) * kD + 2 * lane, r.n0, r.n1);
             if (lane == 0) {
                 st_dev(a.part_m + row * a.nsplit + g0, r.M);
                 st_dev(a.part_l + row * a.nsplit + g0, r.den);

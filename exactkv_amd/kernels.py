@@ -96,14 +96,13 @@ def merge_units(B, Hkv, Hq):
 
 
 FUSED_MERGE_MAX_SPLITS = 1024   # up to this many splits the split kernel can merge in its tail
-# With fused_merge the split kernel's last workgroups merge the partials (two levels of
-# about sqrt(nsplit) splits each; one level up to 8 splits, with the separate merge's
-# bits), writing them with device-scope stores so that no L2 write-back is needed.
+# With fused_merge the split kernel's last workgroups merge the partials (one level up to
+# 32 splits, with the separate merge's bits; beyond, two levels of about sqrt(nsplit)
+# splits each), writing them with device-scope stores so that no L2 write-back is needed.
 # It is not the default: measured on MI355X it costs more than the separate merge launch
-# (eager calls: c2a 53.8 vs 44.6 us, c1 38.4 vs 19.8): every workgroup waits for its
-# stores and an arrival atomic before it can retire, and the last one of a unit then
-# loads and merges the partials, round trips that the separate launch spreads over many
-# workgroups.
+# (eager calls: c2a 47.7 vs 44.4 us, c1 35.0 vs 19.9): after its last page the last
+# workgroup of a unit waits for its stores, an arrival atomic, the partials' loads and the
+# output store, device-scope round trips in a row that cost more than a second launch.
 
 
 def release_workspaces():

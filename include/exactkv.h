@@ -238,10 +238,10 @@ int exkv_decode_to_bf16_paged(const void* sm, const void* code, const void* base
  * q [B, Hq, D] bf16; out [B, Hq, D] bf16; workspace ws_o [B*Hq, nsplit, D],
  * ws_m, ws_l [B*Hq, nsplit] f32, and ws_cnt: exkv_merge_counters(B, Hq, Hkv, nsplit) i32
  * arrival counters, all zero before the first call (each call leaves them zero). With
- * ws_cnt (and nsplit <= 1024) the merge runs inside the split kernel: the last workgroups
- * of each unit merge groups of about sqrt(nsplit) splits, then the groups (one level, with
- * the separate merge's bits, up to 8 splits); without it, as a second kernel. Calls that
- * share a workspace must not overlap.
+ * ws_cnt (and nsplit <= 1024) the merge runs inside the split kernel: the last workgroup of
+ * each unit merges its splits (one level, with the separate merge's bits, up to 32 splits;
+ * beyond, groups of about sqrt(nsplit) splits, then the groups); without it, as a second
+ * kernel. Calls that share a workspace must not overlap.
  * Tokens [0, T) of every sequence, or [0, lens[b*lens_stride])
  * when lens != NULL (then nsplit*split_len must cover TS). split_len: a positive multiple
  * of 16.

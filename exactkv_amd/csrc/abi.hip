@@ -98,19 +98,32 @@ extern "C" int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, i
     return EXKV_OK;
 }
 
-// Split plan of the head-dim 64 / 256 kernels: their workgroups cover one KV head and one
-// group of 16 query heads. Rounds are counted in 512 workgroups, two per CU (the GPU holds
-// three at head dim 64, two at 256, by their LDS rings); with fewer units than that, head
-// dim 64 fills all three slots of every CU (768 workgroups). Measured at the c2a shape (B8 x
-// 8192, 32q/8kv, split kernel): at 64, 12 splits 32.1 us against 33.0 / 34.9 / 34.5 for 8 /
-// 16 / 24; at 256, 8 splits 88.3 us against 153.1 / 95.0 for 4 / 16. Head dim 128: the plan
-// of exkv_plan_splits with its defaults.
+// Split plan per head dim. 128: the plan of exkv_plan_splits with its defaults. 64 with an
+// even number of KV heads runs the head-dim-128 kernel structure over pairs of heads
+// (virtual heads of 128 bytes per row): the same plan over Hkv / 2 virtual heads, a
+// workgroup covering min(gcd(Hkv / 2, 8), 4) of them. Otherwise (256, or 64 with an odd
+// count) the generic kernel, whose workgroups cover one KV head and one group of 16 query
+// heads: rounds are counted in 512 workgroups, two per CU (the GPU holds three at head dim
+// 64, two at 256, by their LDS rings); with fewer units than that, head dim 64 fills all
+// three slots of every CU (768 workgroups). Measured at the c2a shape (B8 x 8192, 32q/8kv,
+// split kernel): at 256, 8 splits 88.3 us against 153.1 / 95.0 for 4 / 16.
 extern "C" int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t D, int32_t* nsplit,
                                    int32_t* split_len) {
     EXKV_REQUIRE(exkv::head_dim_ok(D), "plan_splits_hd: head dim must be 64, 128 or 256 (got %d)", D);
     if (D == 128) return exkv_plan_splits(B, Hkv, Hq, T, 0, 0, nsplit, split_len);
     EXKV_REQUIRE(B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && T > 0, "plan_splits_hd: bad arguments");
     EXKV_REQUIRE(nsplit && split_len, "plan_splits_hd: null output");
+    if (D == 64 && Hkv % 2 == 0) {
+        int hw = Hkv / 2, m = 8;                       // virtual heads per workgroup: gcd(Hkv / 2, 8), at most 4
+        while (m) {
+            const int t = hw % m;
+            hw = m;
+            m = t;
+        }
+        if (hw > 4) hw = 4;
+        plan_core((int64_t)B * (Hkv / 2 / hw) * ((Hq / Hkv + 15) / 16), T, 256, exkv::kPage, nsplit, split_len);
+        return EXKV_OK;
+    }
     const int64_t units = (int64_t)B * Hkv * ((Hq / Hkv + 15) / 16);
     plan_core(units, T, D == 64 && units < 512 ? 768 : 512, 64, nsplit, split_len);
     return EXKV_OK;

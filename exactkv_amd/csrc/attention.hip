@@ -1813,6 +1813,611 @@ __global__ void __launch_bounds__(64) attn_reduce_d_kernel(const float* po, cons
     }
 }
 
+// ---- head dim 64 as pairs of KV heads (attn_pair_kernel)
+//
+// KV heads 2v and 2v + 1 of a token row are 64 + 64 contiguous bytes of sm, 32 + 32 of
+// codes (64 + 64 of base per page, 128 + 128 bytes of a bf16 row): "virtual head" v has
+// the byte layout of one head-dim-128 head. The head-dim-128 split kernels' workgroup
+// structure, loader wavefronts, DMA pattern, ring and flags serve the pairs as they are,
+// with Hkv / 2 virtual heads (a workgroup covers HW of them: min(gcd(Hkv / 2, 8), 4)), so
+// every load moves the pair's 128-byte sm and 64-byte code rows; what differs is the
+// compute side:
+//   * lane (token r, channel group g) takes channels 8g..8g+7 and 32+8g..32+8g+7 of both
+//     heads: its PageBytes hold head 2v's 8 bytes, then head 2v+1's, so rebuild_values
+//     gives out[0..3] = head 2v channels 8g.., out[4..7] = head 2v+1's, out[8..11] = head
+//     2v channels 32+8g.., out[12..15] = head 2v+1's;
+//   * a head's scores are two MFMA k-blocks of its own channels (no product crosses the
+//     heads), with its own group of query heads as the columns; one online softmax each;
+//   * the V tile holds the pair in virtual-channel order (head 2v, then 2v+1), so the
+//     V^T reads of the head-dim-128 kernels give channel blocks 0-3 of head 2v and 4-7 of
+//     head 2v+1;
+//   * metadata and raw rows per real head: up to kRawPair raw rows (128 bytes each) of a
+//     page travel through the wavefront's raw slot, in the order 2v K, 2v V, 2v+1 K, 2v+1 V;
+//   * partials per real head (64 channels), merged by attn_reduce_d_kernel<64>, or the
+//     output itself for one split.
+// The compressed kernel and its bf16 twin share the per-page arithmetic: same bits.
+constexpr int kDp = 64;
+constexpr int kRawPair = 4;
+static_assert(kRawPair * 2 * kDp <= kRawSlot, "a raw slot holds kRawPair head-dim-64 rows");
+
+struct PairMeta {
+    PageMeta h[2];
+};
+__device__ inline int pair_raw_rows(const PairMeta& m) { return raw_rows_of(m.h[0]) + raw_rows_of(m.h[1]); }
+__device__ inline bool pair_raw_in_ring(const PairMeta& m) {
+    const int n = pair_raw_rows(m);
+    return n > 0 && n <= kRawPair;
+}
+__device__ inline int pair_raw_loads(const PairMeta& m) { return pair_raw_in_ring(m) ? 1 : 0; }
+
+// Per-lane LDS offsets of the pair layout within a stage (the loader's swizzles: sm rows
+// of 128 bytes with 16-byte unit u at u ^ (r & 7), code rows of 64 bytes with unit u at
+// u ^ ((r >> 1) & 3), base unswizzled, V tile and staged bf16 V rows with unit u at
+// u ^ ((r & 3) << 1), bf16 K rows with unit u at u ^ (r & 7)).
+struct PairLane {
+    uint32_t sm[4];       // 8-byte pieces: head 2v channels 8g.., 2v+1's, 2v's 32+8g.., 2v+1's
+    uint32_t code[2];     // code bytes 8g..8g+7 of head 2v, of 2v+1
+    uint32_t base[4];     // base bytes, in the order of sm
+    uint32_t tw[2];       // V tile row r: units g, 4+g (+128: 8+g, 12+g)
+    uint32_t bk[4];       // bf16 K row r: units g, 8+g, 4+g, 12+g
+};
+
+__device__ inline PairLane pair_lane_offsets(int r, int g) {
+    PairLane o;
+    const int x7 = r & 7, xc = (r >> 1) & 3, xt = (r & 3) << 1, half = 8 * (g & 1), gu = g >> 1;
+    const int smu[4] = {gu, 4 + gu, 2 + gu, 6 + gu};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.sm[i] = (uint32_t)(r * 128 + 16 * (smu[i] ^ x7) + half);
+    o.code[0] = (uint32_t)(r * 64 + 16 * (gu ^ xc) + half);
+    o.code[1] = (uint32_t)(r * 64 + 16 * ((2 + gu) ^ xc) + half);
+    o.base[0] = (uint32_t)(8 * g);
+    o.base[1] = (uint32_t)(64 + 8 * g);
+    o.base[2] = (uint32_t)(32 + 8 * g);
+    o.base[3] = (uint32_t)(96 + 8 * g);
+    o.tw[0] = (uint32_t)(r * 256 + 16 * (g ^ xt));
+    o.tw[1] = (uint32_t)(r * 256 + 16 * ((4 + g) ^ xt));
+    const int bku[4] = {g, 8 + g, 4 + g, 12 + g};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.bk[j] = (uint32_t)(r * 256 + 16 * (bku[j] ^ x7));
+    return o;
+}
+
+__device__ inline void stage_bytes_pair(uint32_t sb, const PairLane& o, int sm_off, int code_off, int base_off,
+                                        PageBytes& pb) {
+    const uint2 s0 = lds8(lds_ptr(sb + o.sm[0]) + sm_off), s1 = lds8(lds_ptr(sb + o.sm[1]) + sm_off);
+    const uint2 s2 = lds8(lds_ptr(sb + o.sm[2]) + sm_off), s3 = lds8(lds_ptr(sb + o.sm[3]) + sm_off);
+    const uint2 c0 = lds8(lds_ptr(sb + o.code[0]) + code_off), c1 = lds8(lds_ptr(sb + o.code[1]) + code_off);
+    const lds_u8* bp = lds_ptr(sb) + base_off;
+    const uint2 b0 = lds8(bp + o.base[0]), b1 = lds8(bp + o.base[1]), b2 = lds8(bp + o.base[2]),
+                b3 = lds8(bp + o.base[3]);
+    pb.sm_lo = make_uint4(s0.x, s0.y, s1.x, s1.y);
+    pb.sm_hi = make_uint4(s2.x, s2.y, s3.x, s3.y);
+    pb.code = make_uint4(c0.x, c0.y, c1.x, c1.y);
+    pb.b_lo = make_uint4(b0.x, b0.y, b1.x, b1.y);
+    pb.b_hi = make_uint4(b2.x, b2.y, b3.x, b3.y);
+}
+
+__device__ inline void stage_bf16_k_pair(uint32_t sb, const PairLane& o, uint32_t out[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint4 v = lds16(lds_ptr(sb + o.bk[j]) + BS_K);
+        out[4 * j] = v.x; out[4 * j + 1] = v.y; out[4 * j + 2] = v.z; out[4 * j + 3] = v.w;
+    }
+}
+
+__device__ inline void write_v_tile_pair(uint32_t sb, const PairLane& o, int toff, const uint32_t v[16]) {
+    lds_u8* p0 = lds_ptr(sb + o.tw[0]) + toff;         // head 2v channels 8g.. (+128: head 2v+1's)
+    lds_u8* p1 = lds_ptr(sb + o.tw[1]) + toff;         // head 2v channels 32+8g.. (+128: head 2v+1's)
+    lds_st16(p0, v[0], v[1], v[2], v[3]);
+    lds_st16(p1, v[8], v[9], v[10], v[11]);
+    lds_st16(p0 + 128, v[4], v[5], v[6], v[7]);
+    lds_st16(p1 + 128, v[12], v[13], v[14], v[15]);
+}
+
+// The page pair's raw rows into raw_st when they travel through the ring: entry e = lane /
+// 8 (8 lanes x 16 bytes per 128-byte row), K rows of head 2v, its V rows, then head 2v+1's.
+__device__ inline void dma_pair_raw(int lane, const PairMeta& m, uint32_t raw_st, const PairSrc& rawp,
+                                    const PairSrc& rawn) {
+    if (!pair_raw_in_ring(m)) return;                  // uniform
+    // the slot was last read by this wavefront's splice of two pages back
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int e = lane >> 3;
+    const int n0k = __builtin_popcount(m.h[0].mk), n0 = n0k + __builtin_popcount(m.h[0].mv);
+    const int n1k = n0 + __builtin_popcount(m.h[1].mk), n = n1k + __builtin_popcount(m.h[1].mv);
+    const bool isv = (e >= n0k && e < n0) || e >= n1k;
+    const int32_t off = e < n0k ? m.h[0].ok + e
+                      : e < n0  ? m.h[0].ov + (e - n0k)
+                      : e < n1k ? m.h[1].ok + (e - n0)
+                                : m.h[1].ov + (e - n1k);
+    bool bad;
+    const int64_t idx = clamp_slot((int64_t)off, (int64_t)rawn.pick(isv), bad);
+    if (lane < 8 * n) {
+        if (bad) report_error(kErrRawSlot);
+        dma16((const void*)(uintptr_t)(rawp.pick(isv) + (uint64_t)idx * (2 * kDp) + (uint64_t)(lane & 7) * 16), raw_st);
+    }
+}
+
+// Splice the pair's raw K (V = false) or V rows into the lane's values: head k's are
+// d[4k..4k+3] (channels 8g..) and d[8+4k..] (32+8g..). From the raw slot when the page's
+// rows came through the ring, else straight from the pool (rare; waits for every load).
+template <bool V>
+__device__ inline void splice_pair(const AttnArgs& a, const PairMeta& m, uint32_t slot, int r, int g,
+                                   uint32_t d[16]) {
+    const uint32_t below = (1u << r) - 1u;
+    const bool ring = pair_raw_in_ring(m);
+    int e0 = 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const PageMeta& mh = m.h[k];
+        const uint32_t mask = V ? mh.mv : mh.mk;
+        if (mask != 0u) {                              // uniform
+            uint32_t x[8];
+            if (ring) {
+                const int e = e0 + (V ? __builtin_popcount(mh.mk) : 0) + __builtin_popcount(mask & below);
+                const lds_u8* p = lds_ptr(slot + (uint32_t)(min(e, kRawPair - 1) * 2 * kDp));
+                const uint4 lo = lds16(p + 16 * g), hi = lds16(p + 64 + 16 * g);
+                x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+                x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+            } else {
+                const CSrc& c = V ? a.v : a.k;
+                const int64_t sl = raw_slot(mask, V ? mh.ov : mh.ok, r, c.raw_rows);
+                const uint8_t* rp = reinterpret_cast<const uint8_t*>(c.raw + sl * kDp);
+                const uint4 lo = ld16(rp + 16 * g), hi = ld16(rp + 64 + 16 * g);
+                x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+                x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+                wait_vm<0>();
+                settle(x);
+            }
+            const bool take = ((mask >> r) & 1u) != 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                d[4 * k + i] = take ? x[i] : d[4 * k + i];
+                d[8 + 4 * k + i] = take ? x[4 + i] : d[8 + 4 * k + i];
+            }
+        }
+        e0 += raw_rows_of(mh);
+    }
+}
+
+// q of the pair's query heads through LDS: head 2v + k's (k = 0, 1) query heads hg*16 + i,
+// i < gh, at qst + 2048 k + 128 i (64 channels), by direct-to-LDS loads of 8 rows each.
+__device__ inline void q_dma_pair(const AttnArgs& a, int b, int hk0, int hg, int gh, int lane, uint32_t qst) {
+    const int nq = (gh + 7) >> 3;
+    for (int k = 0; k < 2; ++k)
+        for (int d = 0; d < nq; ++d) {
+            const int i = min(8 * d + (lane >> 3), gh - 1);
+            dma16(a.q + ((int64_t)b * a.Hq + (int64_t)(hk0 + k) * a.G + hg * 16 + i) * kDp + 8 * (lane & 7),
+                  qst + (uint32_t)(2048 * k + 1024 * d));
+        }
+}
+
+// Q^T operands: qop[2k + j] = head 2v + k's query head r (column), channels 8g + 32j ..
+// 8g + 32j + 7 (the k-elements lane group g supplies); heads past the group are zero.
+__device__ inline void load_qop_pair(uint32_t qst, int r, int g, int gh, bf16x8 (&qop)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int k = i >> 1, j = i & 1;
+        uint4 v = lds16(lds_ptr(qst + (uint32_t)(2048 * k + r * 128 + 2 * (8 * g + 32 * j))));
+        if (r >= gh) v = make_uint4(0u, 0u, 0u, 0u);
+        qop[i] = as_bf16x8(v.x, v.y, v.z, v.w);
+        asm volatile("" : "+v"(qop[i]));
+    }
+}
+
+// Each head's score MFMAs, over its own channels: head 2v's k-blocks are out[0..3] and
+// out[8..11], head 2v+1's out[4..7] and out[12..15]
+__device__ inline void pair_scores(const uint32_t (&kd)[16], const bf16x8 (&qop)[4], f32x4& s0, f32x4& s1) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[0], kd[1], kd[2], kd[3]), qop[0], z, 0, 0, 0);
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[8], kd[9], kd[10], kd[11]), qop[1], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[4], kd[5], kd[6], kd[7]), qop[2], z, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kd[12], kd[13], kd[14], kd[15]), qop[3], s1, 0, 0, 0);
+}
+
+// One page of the pair after its scores: V^T operands of both heads, then each head's
+// online softmax and P.V (head 2v, then 2v+1)
+__device__ __forceinline__ void pair_softmax_pv(const f32x4& s0, const f32x4& s1, const s16x4 (&vt)[8], bool ragged,
+                                                int t0, const SplitCoords& c, int g, float qk_scale, float (&m_i)[2],
+                                                float (&l_i)[2], f32x4 (&acc0)[4], f32x4 (&acc1)[4]) {
+    const s16x4 v0[4] = {vt[0], vt[1], vt[2], vt[3]}, v1[4] = {vt[4], vt[5], vt[6], vt[7]};
+    page_softmax_pv<4>(s0, v0, ragged, t0, c.end, c.wlo, g, qk_scale, m_i[0], l_i[0], acc0);
+    page_softmax_pv<4>(s1, v1, ragged, t0, c.end, c.wlo, g, qk_scale, m_i[1], l_i[1], acc1);
+}
+
+// Partials of the pair: a head's row in LDS is kMoRowP floats (64 channels, padded)
+constexpr int kMoRowP = kDp + 4;
+constexpr int kMoHeadP = (16 * kMoRowP + 32) * 4;      // bytes of one head's partial (o, then m[16], l[16])
+static_assert(Ring<true>::per_wave >= 2 * kMoHeadP && Ring<false>::per_wave >= 2 * kMoHeadP,
+              "a page phase's partials of both heads fit its wavefront's ring");
+
+// One split per row: the output with the merge's arithmetic for a single term (as
+// store_direct; attn_reduce_d_kernel<64> at ns = 1 gives the same bits)
+__device__ inline void store_direct_d64(const AttnArgs& a, int64_t orow, int g, const f32x4 (&o)[4], float m,
+                                        float l) {
+    const float w = fast_exp2(m - m);
+    const float den = __builtin_fmaf(l, w, 0.f);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        float n[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) n[k] = __builtin_fmaf(o[nb][k], w, 0.f);
+        *reinterpret_cast<uint2*>(a.out + orow * kDp + 16 * nb + 4 * g) =
+            make_uint2(pack_bf16x2(n[0] / den, n[1] / den), pack_bf16x2(n[2] / den, n[3] / den));
+    }
+}
+
+// After the page loop: both heads' partials per (split, query head), page phases merged as
+// in split_epilogue (phase p > 0 leaves its partials in its ring and raises done[wave];
+// phase 0 waits, bounded, and merges in phase order).
+__device__ __forceinline__ void pair_epilogue(const AttnArgs& a, const SplitCoords& c, int HWv, uint32_t ring0,
+                                              uint32_t ring_stride, int* done, int wave, int lane, bool active,
+                                              int hk0, int gh, const f32x4 (&acc0)[4], const f32x4 (&acc1)[4],
+                                              const float (&m_i)[2], const float (&l_i)[2]) {
+    const int r = lane & 15, g = lane >> 4;
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    const float lt[2] = {group_sum(l_i[0]), group_sum(l_i[1])};
+    const int phase = wave >> c.hw_sh;
+    auto mo = [&](int w, int k) { return ring0 + (uint32_t)w * ring_stride + (uint32_t)(k * kMoHeadP); };
+    auto ld_ml = [&](int w, int k, int which) {
+        return *reinterpret_cast<const EXKV_LDS float*>(lds_ptr(mo(w, k) + 4u * (16 * kMoRowP + 16 * which + r)));
+    };
+    if (active && phase > 0) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const f32x4(&acc)[4] = k ? acc1 : acc0;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                *reinterpret_cast<EXKV_LDS f32x4*>(lds_ptr(mo(wave, k) + 4u * (r * kMoRowP + 16 * nb + 4 * g))) = acc[nb];
+            if (g == 0) {
+                *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave, k) + 4u * (16 * kMoRowP + r))) = m_i[k];
+                *reinterpret_cast<EXKV_LDS float*>(lds_ptr(mo(wave, k) + 4u * (16 * kMoRowP + 16 + r))) = lt[k];
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_flag_st(&done[wave], 1);
+    } else if (active && r < gh) {
+        for (int ph = 1; ph < c.nphase; ++ph) {
+            const int w = ph * HWv + wave;
+            int s = 0;
+            for (; s < a.spin && lds_flag_ld(&done[w]) == 0; ++s) __builtin_amdgcn_s_sleep(1);
+            if (s == a.spin) report_error(kErrWait);
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const f32x4(&acc)[4] = k ? acc1 : acc0;
+            float M = fmaxf(-INFINITY, m_i[k]);
+            for (int ph = 1; ph < c.nphase; ++ph) M = fmaxf(M, ld_ml(ph * HWv + wave, k, 0));
+            f32x4 o[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            float l = 0.f;
+            if (M != -INFINITY) {
+                const float wt = fast_exp2(m_i[k] - M);
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) o[nb][q] += wt * acc[nb][q];
+                l += wt * lt[k];
+                for (int ph = 1; ph < c.nphase; ++ph) {
+                    const int w = ph * HWv + wave;
+                    const float wp = fast_exp2(ld_ml(w, k, 0) - M);
+#pragma unroll
+                    for (int nb = 0; nb < 4; ++nb) {
+                        const f32x4 v = *reinterpret_cast<const EXKV_LDS f32x4*>(
+                            lds_ptr(mo(w, k) + 4u * (r * kMoRowP + 16 * nb + 4 * g)));
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) o[nb][q] += wp * v[q];
+                    }
+                    l += wp * ld_ml(w, k, 1);
+                }
+            }
+            const int64_t orow = (int64_t)c.b * a.Hq + (int64_t)(hk0 + k) * a.G + c.hg * 16 + r;
+            if (a.nsplit == 1 && a.out != nullptr) {
+                store_direct_d64(a, orow, g, o, M, l);
+            } else {
+                const int64_t prow = orow * a.nsplit + c.split;
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) *reinterpret_cast<f32x4*>(a.part_o + prow * kDp + 16 * nb + 4 * g) = o[nb];
+                if (g == 0) {
+                    a.part_m[prow] = M;
+                    a.part_l[prow] = l;
+                }
+            }
+        }
+    }
+}
+
+template <bool COMP>
+__global__ void attn_pair_kernel(AttnArgs a);
+
+// Compressed: the structure of attn_split_kernel<true> (8 compute + 2 loader wavefronts)
+template <>
+__global__ void __launch_bounds__(kCompThreads) attn_pair_kernel<true>(AttnArgs ar) {
+    constexpr int NST = Ring<true>::nst, STB = Ring<true>::stage;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<true>::bytes];
+    __shared__ int progress[kWaves];                   // pages done per compute wavefront (priority hint)
+    __shared__ int ready[kWaves];                      // pages of wavefront w in its ring (loader -> w)
+    __shared__ int avail[kWaves];                      // pages of w its loader may issue (w -> loader)
+    __shared__ int done[kWaves];                       // page phase p > 0: partials left in the ring
+    AttnArgs a = ar;                                   // virtual heads: the loader and coordinates see pairs
+    a.Hkv = ar.Hkv / 2;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);    // uniform: scalar addressing
+    const SplitCoords c = split_coords(a);
+    const int hv = c.hb * a.HW + (wave & (a.HW - 1));  // virtual head: KV heads 2hv, 2hv + 1
+    const int hk0 = 2 * hv;
+    const int gh = min(16, ar.G - c.hg * 16);
+    if (threadIdx.x < kWaves) {
+        ready[threadIdx.x] = 0;
+        avail[threadIdx.x] = NST - 1;                  // the last stage holds q and the page table at first
+        done[threadIdx.x] = 0;
+    }
+    __syncthreads();
+
+    float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (wave >= kWaves) {
+        comp_loader(a, c, lds_addr(lds), ready, avail, wave - kWaves, lane);
+    } else {
+        const int phase = wave >> c.hw_sh;
+        const int npw = c.npw(phase);
+        const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<true>::per_wave);   // this wave's (uniform)
+        const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
+        const PairLane po = pair_lane_offsets(r, g);
+        const LdsLane lo = lds_lane_offsets(r, g);     // the V^T reads
+        const PairSrc rawp = pair_src((uint64_t)(uintptr_t)ar.k.raw, (uint64_t)(uintptr_t)ar.v.raw);
+        const PairSrc rawn = pair_src((uint64_t)ar.k.raw_rows, (uint64_t)ar.v.raw_rows);
+
+        // metadata of both heads of the wavefront's pages: lane i holds page i's (i < 64),
+        // loaded once with q by direct-to-LDS loads, then v_readlane per page (scalar loads
+        // past 64); the same for the block-table entries of a paged cache
+        int32_t vbt = 0;
+        auto gpage = [&](int j) -> int64_t {
+            const int lp = c.p0 + phase + c.nphase * j;
+            int32_t e = 0;
+            if (ar.block_table != nullptr)
+                e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(ar.block_table + c.b * ar.bt_stride + lp);
+            return array_page(a, c, lp, e);
+        };
+        uint32_t vmk[2] = {0u, 0u}, vmv[2] = {0u, 0u};
+        int32_t vok[2] = {0, 0}, vov[2] = {0, 0};
+        auto meta = [&](int j) {
+            PairMeta m;
+            if (j >= 64) {
+                const int64_t gp = gpage(j);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int64_t page = gp * ar.Hkv + hk0 + k;
+                    m.h[k] = PageMeta{(uint32_t)const_ld(ar.k.rowmask + page), (uint32_t)const_ld(ar.v.rowmask + page),
+                                      const_ld(ar.k.rowoff + page), const_ld(ar.v.rowoff + page)};
+                }
+                return m;
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                m.h[k] = PageMeta{(uint32_t)__builtin_amdgcn_readlane((int)vmk[k], j),
+                                  (uint32_t)__builtin_amdgcn_readlane((int)vmv[k], j),
+                                  __builtin_amdgcn_readlane(vok[k], j), __builtin_amdgcn_readlane(vov[k], j)};
+            return m;
+        };
+        auto issue_raw = [&](int j, const PairMeta& m) {
+            dma_pair_raw(lane, m, raw_ring + (uint32_t)((j & 1) * kRawSlot), rawp, rawn);
+        };
+        // q (4 KiB) and the metadata (2 KiB) through the last stage, which no page uses before
+        // the wavefront hands it over (avail = NST below)
+        const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
+        const uint32_t mst = qst + 4096u;              // per head (+1024): rowmask K | rowoff K | rowmask V | rowoff V
+        const int i_pg = min(lane, max(npw - 1, 0));   // per lane: the wavefront's page i
+        if (ar.block_table != nullptr) {               // the block-table entries first: every address needs them
+            const uint32_t bst = mst + 2048u;
+            dma4(ar.block_table + c.b * ar.bt_stride + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1), bst);
+            wait_vm<0>();
+            vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        q_dma_pair(ar, c.b, hk0, c.hg, gh, lane, qst);
+        {
+            const int64_t gp = ar.block_table == nullptr ? (int64_t)c.b * c.NP + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1)
+                                                         : array_page(a, c, 0, vbt);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t page = gp * ar.Hkv + hk0 + k;
+                const uint32_t mk = mst + 1024u * k;
+                dma4(ar.k.rowmask + page, mk);
+                dma4(ar.k.rowoff + page, mk + 256u);
+                dma4(ar.v.rowmask + page, mk + 512u);
+                dma4(ar.v.rowoff + page, mk + 768u);
+            }
+        }
+        wait_vm<0>();
+        bf16x8 qop[4];
+        load_qop_pair(qst, r, g, gh, qop);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t mk = mst + 1024u * k + 4u * lane;
+            vmk[k] = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mk));
+            vok[k] = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mk + 256u));
+            vmv[k] = *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(mk + 512u));
+            vov[k] = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(mk + 768u));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q and the page table are in registers
+        lds_flag_st(&avail[wave], NST);
+        if (npw > 0) issue_raw(0, meta(0));
+        if (npw > 1) issue_raw(1, meta(1));
+
+        lds_flag_st(&progress[wave], 0);
+        int stg = 0;                                   // stage of page j (j % NST)
+        for (int j = 0; j < npw; ++j) {
+            // page j's raw rows have landed once only page j + 1's are in flight
+            if (j + 1 < npw)
+                wait_vm_n(pair_raw_loads(meta(j + 1)));
+            else
+                wait_vm<0>();
+            if (lds_flag_ld(&ready[wave]) <= j) {      // page j's bytes: published by the loader
+                int s = 0;
+                for (; s < a.spin && lds_flag_ld(&ready[wave]) <= j; ++s) __builtin_amdgcn_s_sleep(0);
+                if (s == a.spin) report_error(kErrWait);
+            }
+            asm volatile("" ::: "memory");
+            const uint32_t sb = ring + (uint32_t)(stg * STB);
+            stg = stg == NST - 1 ? 0 : stg + 1;
+            const int t0 = (c.p0 + phase + c.nphase * j) * kPage;
+            const bool ragged = t0 + kPage > c.end || t0 < c.wlo;   // uniform: a split's last page, or the window's first
+            const bool valid = t0 + r < c.end && t0 + r >= c.wlo;
+            const PairMeta mc = meta(j);
+            const PairMeta mn = j + NST - 1 < npw ? meta(j + NST - 1) : PairMeta{};
+            const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
+            lds_flag_st(&progress[wave], j);
+
+            // V first: its tile is written and its V^T operands read while K is rebuilt
+            PageBytes pk, pv;
+            stage_bytes_pair(sb, po, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
+            stage_bytes_pair(sb, po, CS_KSM, CS_KCODE, CS_BASE, pk);
+            balance_priority(j, other);
+            const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
+            uint32_t kd[16], vd[16];
+            rebuild_values(pv, vd);
+            if ((mc.h[0].mv | mc.h[1].mv) != 0u) {      // page with raw V rows
+                keep_branch();
+                splice_pair<true>(ar, mc, slot, r, g, vd);
+            }
+            if (ragged) {
+                keep_branch();
+                zero_invalid_rows(valid, vd);
+            }
+            write_v_tile_pair(sb, po, Ring<true>::vtile, vd);     // over the K bytes, read above
+            s16x4 vt[8];
+            read_vt(sb, lo, Ring<true>::vtile, vt);
+            rebuild_values(pk, kd);
+            if ((mc.h[0].mk | mc.h[1].mk) != 0u) {
+                keep_branch();
+                splice_pair<false>(ar, mc, slot, r, g, kd);
+            }
+            if (ragged) {
+                keep_branch();
+                zero_invalid_rows(valid, kd);
+            }
+            f32x4 s0, s1;
+            pair_scores(kd, qop, s0, s1);
+            // this page's raw rows are out of their slot: page j + 2's go there
+            if (j + NST - 1 < npw) issue_raw(j + NST - 1, mn);
+            // every LDS read of the stage (bytes, V^T operands) has returned: hand it back
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_flag_st(&avail[wave], j + NST + 1);
+            pair_softmax_pv(s0, s1, vt, ragged, t0, c, g, a.qk_scale, m_i, l_i, acc0, acc1);
+        }
+    }
+    pair_epilogue(ar, c, a.HW, lds_addr(lds), Ring<true>::per_wave, done, wave, lane, wave < kWaves, hk0, gh, acc0,
+                  acc1, m_i, l_i);
+}
+
+// bf16 twin: the structure of attn_split_kernel<false> (8 wavefronts issuing their own pages)
+template <>
+__global__ void __launch_bounds__(kThreads) attn_pair_kernel<false>(AttnArgs ar) {
+    constexpr int NST = Ring<false>::nst, STB = Ring<false>::stage;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[Ring<false>::bytes];
+    __shared__ int progress[kWaves];
+    __shared__ int done[kWaves];                       // page phase p > 0: partials left in the ring
+    AttnArgs a = ar;
+    a.Hkv = ar.Hkv / 2;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const SplitCoords c = split_coords(a);
+    if (threadIdx.x < kWaves) done[threadIdx.x] = 0;
+    __syncthreads();
+    const int hv = c.hb * a.HW + (wave & (a.HW - 1));
+    const int hk0 = 2 * hv;
+    const int gh = min(16, ar.G - c.hg * 16);
+    const int phase = wave >> c.hw_sh;
+    const int npw = c.npw(phase);
+    const int64_t rs = a.Hkv;
+    float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<false>::per_wave);
+    const LdsLane lo = lds_lane_offsets(r, g);
+    const PairLane po = pair_lane_offsets(r, g);
+    const DmaLane dl = dma_lane_offsets<false>(lane, rs);
+    const PairSrc nobase{0ull, 0ull};
+    int32_t vbt = 0;
+    auto gpage = [&](int j) -> int64_t {
+        const int lp = c.p0 + phase + c.nphase * j;
+        int32_t e = 0;
+        if (ar.block_table != nullptr)
+            e = j < 64 ? __builtin_amdgcn_readlane(vbt, j) : const_ld(ar.block_table + c.b * ar.bt_stride + lp);
+        return array_page(a, c, lp, e);
+    };
+    auto issue = [&](int j, uint32_t sb) {
+        const int64_t gp = gpage(j);
+        dma_page_bytes<false>(a, dl, gp * kPage * rs + hv, gp * rs + hv, sb, lane, nobase);
+    };
+    // q through the last stage, which no page uses before page NST - 1 is issued
+    const uint32_t qst = ring + (uint32_t)((NST - 1) * STB);
+    if (ar.block_table != nullptr) {
+        const uint32_t bst = qst + 5120u;
+        const int i_pg = min(lane, max(npw - 1, 0));
+        dma4(ar.block_table + c.b * ar.bt_stride + min(c.p0 + phase + c.nphase * i_pg, c.NP - 1), bst);
+        wait_vm<0>();
+        vbt = *reinterpret_cast<const EXKV_LDS int32_t*>(lds_ptr(bst + 4u * lane));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    q_dma_pair(ar, c.b, hk0, c.hg, gh, lane, qst);
+    if (npw > 0) {
+        issue(0, ring);
+        wait_vm<kDmaPerPage[0]>();                     // q has landed once only page 0's loads are in flight
+    } else {
+        wait_vm<0>();
+    }
+    bf16x8 qop[4];
+    load_qop_pair(qst, r, g, gh, qop);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // q is in registers before its stage is reused
+
+    lds_flag_st(&progress[wave], 0);
+    int stg = 0;
+    for (int j = 0; j < npw; ++j) {
+        wait_vm<0>();                                  // page j has landed (the only page in flight)
+        const uint32_t sb = ring + (uint32_t)(stg * STB);
+        const int stn = stg == 0 ? NST - 1 : stg - 1;  // stage of page j + 1
+        stg = stg == NST - 1 ? 0 : stg + 1;
+        const int t0 = (c.p0 + phase + c.nphase * j) * kPage;
+        const bool ragged = t0 + kPage > c.end || t0 < c.wlo;
+        const bool valid = t0 + r < c.end && t0 + r >= c.wlo;
+        if (j + NST - 1 < npw) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(j + NST - 1, ring + (uint32_t)(stn * STB));
+        }
+        const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
+        lds_flag_st(&progress[wave], j);
+        uint32_t kd[16];
+        stage_bf16_k_pair(sb, po, kd);
+        balance_priority(j, other);
+        if (ragged) {
+            keep_branch();
+            zero_invalid_rows(valid, kd);
+        }
+        f32x4 s0, s1;
+        pair_scores(kd, qop, s0, s1);
+        if (ragged) {                                  // ragged page: zero the staged V rows past the end
+            keep_branch();
+            if (!valid) {
+                uint32_t vd[16];
+                zero_invalid_rows(false, vd);
+                write_v_tile(sb, lo, Ring<false>::vtile, vd);
+            }
+        }
+        s16x4 vt[8];
+        read_vt(sb, lo, Ring<false>::vtile, vt);
+        pair_softmax_pv(s0, s1, vt, ragged, t0, c, g, a.qk_scale, m_i, l_i, acc0, acc1);
+    }
+    pair_epilogue(ar, c, a.HW, lds_addr(lds), Ring<false>::per_wave, done, wave, lane, true, hk0, gh, acc0, acc1,
+                  m_i, l_i);
+}
+
 }  // namespace exkv
 
 using namespace exkv;
@@ -1831,6 +2436,28 @@ static int heads_per_block(int Hkv) {
         b = t;
     }
     return a < 4 ? a : 4;
+}
+
+// Head dim 64 with an even number of KV heads runs as pairs of heads (attn_pair_kernel);
+// odd counts and head dim 256 run attn_dgen_kernel.
+static bool pair_heads(int D, int Hkv) { return D == 64 && Hkv % 2 == 0; }
+
+// KV heads (virtual heads of two, for pairs) per workgroup of the split kernels
+static int block_heads(int D, int Hkv) { return pair_heads(D, Hkv) ? heads_per_block(Hkv / 2) : heads_per_block(Hkv); }
+
+// Workgroup units (sequence, head block, query group) of the split kernels' 2-D grid
+static int64_t grid_units(int B, int Hq, int Hkv, int D) {
+    const int64_t hg = (Hq / Hkv + 15) / 16;
+    if (D == kD) return (int64_t)B * (Hkv / block_heads(D, Hkv)) * hg;
+    if (pair_heads(D, Hkv)) return (int64_t)B * (Hkv / 2 / block_heads(D, Hkv)) * hg;
+    return (int64_t)B * Hkv * hg;                      // the generic kernel's one-dimensional units
+}
+
+// One launch: one split (the split kernel writes the output), or the merge in the split
+// kernel's tail (head dim 128, with arrival counters)
+static bool one_launch(int D, int Hkv, int nsplit, const int32_t* ws_cnt) {
+    if (D == kD) return nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits);
+    return pair_heads(D, Hkv) && nsplit == 1;
 }
 
 static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_t* lens, int nsplit,
@@ -1852,13 +2479,13 @@ static int check_attn(int B, int Hq, int Hkv, int D, int T, int TS, const int32_
         EXKV_REQUIRE((int64_t)nsplit * split_len >= min((int64_t)TS, reach),
                      "attention: with per-sequence lengths the splits must cover TS=%d (window %d)", TS, window);
     }
-    EXKV_REQUIRE((int64_t)B * (D == kD ? Hkv / heads_per_block(Hkv) : Hkv) * ((Hq / Hkv + 15) / 16) < 65536,
-                 "attention: too many (sequence, head block) units");
-    // a launch's grid is 32-bit in work-items: x = splits (head dim 128; the compressed
-    // kernel's workgroups are the larger) or every workgroup (the one-dimensional grid of
-    // the other head dims, DGen<D, *>::NPH wavefronts each)
-    const int64_t wg_x = D == kD ? (int64_t)nsplit : (int64_t)nsplit * B * Hkv * ((Hq / Hkv + 15) / 16);
-    const int64_t wg_threads = D == kD ? kCompThreads : 64 * (D >= 256 ? 2 : 4);
+    EXKV_REQUIRE(grid_units(B, Hq, Hkv, D) < 65536, "attention: too many (sequence, head block) units");
+    // a launch's grid is 32-bit in work-items: x = splits (head dim 128 and pairs of head-dim-64
+    // heads; the compressed kernel's workgroups are the larger) or every workgroup (the
+    // one-dimensional grid of the generic kernel, DGen<D, *>::NPH wavefronts each)
+    const bool two_d = D == kD || pair_heads(D, Hkv);
+    const int64_t wg_x = two_d ? (int64_t)nsplit : (int64_t)nsplit * grid_units(B, Hq, Hkv, D);
+    const int64_t wg_threads = two_d ? kCompThreads : 64 * (D >= 256 ? 2 : 4);
     EXKV_REQUIRE(wg_x * wg_threads <= (int64_t)UINT32_MAX, "attention: too many workgroups (%d splits)", nsplit);
     return EXKV_OK;
 }
@@ -1885,6 +2512,16 @@ static int launch_split(bool comp, const AttnArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * (a.Hkv / a.HW) * a.HG));
     hipEvent_t e0 = t_split_start, e1 = t_split_stop;
     t_split_start = t_split_stop = nullptr;
+    if (pair_heads(a.D, a.Hkv)) {
+        const dim3 pgrid((unsigned)a.nsplit, (unsigned)(a.B * (a.Hkv / 2 / a.HW) * a.HG));
+        auto k = comp ? attn_pair_kernel<true> : attn_pair_kernel<false>;
+        const dim3 block(comp ? kCompThreads : kThreads);
+        if (e0 || e1)
+            hipExtLaunchKernelGGL(k, pgrid, block, 0, stream, e0, e1, 0, a);
+        else
+            hipLaunchKernelGGL(k, pgrid, block, 0, stream, a);
+        return hip_status(hipGetLastError(), comp ? "attn_split_compressed" : "attn_split_bf16");
+    }
     if (a.D != kD) {
         if (a.D == 64)
             launch_dgen<64>(comp, a, e0, e1, stream);
@@ -1965,7 +2602,7 @@ static int fill_compressed(AttnArgs& a, const void* q, const void* k_sm, const v
     a.lens = lens; a.lens_stride = lens_stride;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
-    a.HW = heads_per_block(Hkv);
+    a.HW = block_heads(D, Hkv);
     a.D = D;
     a.spin = t_wait_limit;
     return EXKV_OK;
@@ -1985,7 +2622,7 @@ static int fill_bf16(AttnArgs& a, const void* q, const void* k, const void* v, f
     a.lens = lens; a.lens_stride = lens_stride;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.HG = (a.G + 15) / 16; a.TS = TS; a.T = T;
     a.nsplit = nsplit; a.split_len = split_len; a.window = window; a.qk_scale = qk_scale;
-    a.HW = heads_per_block(Hkv);
+    a.HW = block_heads(D, Hkv);
     a.D = D;
     a.spin = t_wait_limit;
     return EXKV_OK;
@@ -2010,7 +2647,7 @@ extern "C" int exkv_attn_compressed(EXKV_C_PARAMS, int32_t* ws_cnt, void* out, E
     int rc = fill_compressed(a, EXKV_C_ARGS, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed: null output");
-    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+    if (one_launch(D, Hkv, nsplit, ws_cnt)) {
         // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
         a.counters = nsplit > 1 ? ws_cnt : nullptr;
@@ -2032,7 +2669,7 @@ extern "C" int exkv_attn_bf16(const void* q, const void* k, const void* v, float
     int rc = fill_bf16(a, q, k, v, ws_o, ws_m, ws_l, EXKV_SHAPE_ARGS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16: null output");
-    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+    if (one_launch(D, Hkv, nsplit, ws_cnt)) {
         // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
         a.counters = nsplit > 1 ? ws_cnt : nullptr;
@@ -2072,7 +2709,7 @@ extern "C" int exkv_attn_compressed_paged(EXKV_C_PARAMS, int32_t* ws_cnt, void* 
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_compressed_paged: null output");
-    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+    if (one_launch(D, Hkv, nsplit, ws_cnt)) {
         // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
         a.counters = nsplit > 1 ? ws_cnt : nullptr;
@@ -2098,7 +2735,7 @@ extern "C" int exkv_attn_bf16_paged(const void* q, const void* k, const void* v,
     if (!rc) rc = set_paged(a, block_table, bt_stride, pool_pages, TS);
     if (rc) return rc;
     EXKV_REQUIRE(out, "attn_bf16_paged: null output");
-    if (D == kD && (nsplit == 1 || (ws_cnt && nsplit <= kFusedMaxSplits))) {
+    if (one_launch(D, Hkv, nsplit, ws_cnt)) {
         // one launch: one split (the output directly), or the merge in the split kernel's tail
         a.out = (uint16_t*)out;
         a.counters = nsplit > 1 ? ws_cnt : nullptr;

@@ -49,9 +49,13 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == 1 and b"outside the cache" in lib.exkv_last_error()
     with pytest.raises(RuntimeError, match="split_len"):
         _lib.call("exkv_attn_bf16", 1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 100, 128, None, 0, 4, 30, 0, 0.1, None)
-    # grids past 2^32 work-items: 1024 splits x 4096 x 8 workgroups of 256 threads (head
-    # dim 64), 7M splits of 640-thread workgroups (head dim 128)
-    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 4096, 32, 8, 64, 16384, 16384, None, 0, 1024, 16, 0, 0.1, None)
+    # grids past 2^32 work-items: 1024 splits x 4096 x 7 workgroups of 256 threads (head dim
+    # 64 with an odd KV-head count: the generic kernel's one-dimensional grid), 7M splits of
+    # 640-thread workgroups (head dim 128; 64 with an even count takes the same grid)
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 4096, 28, 7, 64, 16384, 16384, None, 0, 1024, 16, 0, 0.1, None)
+    assert rc == 1 and b"too many workgroups" in lib.exkv_last_error()
+    rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 64, 112000000, 112000000, None, 0, 7000000, 16, 0,
+                            0.1, None)
     assert rc == 1 and b"too many workgroups" in lib.exkv_last_error()
     rc = lib.exkv_attn_bf16(1, 1, 1, 1, 1, 1, None, 1, 1, 32, 8, 128, 112000000, 112000000, None, 0, 7000000, 16, 0,
                             0.1, None)
@@ -94,21 +98,24 @@ def test_plan_splits(B, Hkv, Hq, T, expect):
 
 
 @pytest.mark.parametrize("B,Hkv,Hq,T,D,expect", [
-    (8, 8, 32, 8192, 64, (12, 704)),     # 64 units (one per KV head) x 12 = 768 workgroups (three per CU)
+    (8, 8, 32, 8192, 64, (32, 256)),     # pairs of heads: 4 virtual heads = one block per sequence, 8 units x 32
     (8, 8, 32, 8192, 256, (8, 1024)),    # 64 units x 8 = 512 workgroups (two per CU)
-    (32, 2, 14, 4096, 64, (12, 352)),    # Qwen2.5-0.5B shape: 64 units
+    (32, 2, 14, 4096, 64, (8, 512)),     # Qwen2.5-0.5B shape: one virtual head, 32 units x 8
     (1, 8, 32, 131072, 256, (64, 2048)),
-    (2, 2, 64, 1000, 64, (16, 64)),      # G = 32: two head groups per KV head, 8 units; capped by 64-token splits
-    (600, 8, 32, 4096, 64, (2, 2048)),   # 4800 units, 9.4 rounds: two splits fill the last round to 98.7%
+    (2, 2, 64, 1000, 64, (63, 16)),      # G = 32: two query groups, 4 units; one page per split
+    (600, 8, 32, 4096, 64, (5, 832)),    # 600 units: the first split count whose last round is >= 95% full
+    (8, 7, 28, 8192, 64, (14, 608)),     # odd KV-head count: the generic kernel, 56 units, 768 workgroups
     (8, 8, 32, 8192, 128, (16, 512)),    # head dim 128: exkv_plan_splits
 ])
 def test_plan_splits_hd(B, Hkv, Hq, T, D, expect):
     from exactkv_amd.kernels import plan_splits, plan_splits_hd
     ns, sl = plan_splits_hd(B, Hkv, Hq, T, D)
     assert (ns, sl) == expect
-    assert sl % 32 == 0 and ns * sl >= T and (ns - 1) * sl < T
+    assert (sl % 32 == 0 or sl == 16) and ns * sl >= T and (ns - 1) * sl < T
     if D == 128:
         assert (ns, sl) == plan_splits(B, Hkv, Hq, T)
+    if D == 64 and Hkv % 2 == 0:                     # pairs: the head-dim-128 plan over Hkv / 2 virtual heads
+        assert (ns, sl) == plan_splits(B, Hkv // 2, Hq // 2, T)
 
 
 def test_rebuild_bitmath_exhaustive(tmp_path):

@@ -34,8 +34,9 @@ def choose_split(B, Hkv, T, BLOCK_N, target=512):
 
 
 def plan_splits_hd(B, Hkv, Hq, T, D):
-    """Split plan for head dim D (exkv_plan_splits_hd): plan_splits' defaults at 128, one
-    round of the generic-head-dim kernel's workgroups at 64 and 256."""
+    """Split plan for head dim D (exkv_plan_splits_hd): plan_splits' defaults at 128 and,
+    over Hkv / 2 pairs of KV heads, at 64 with an even Hkv; rounds of the generic-head-dim
+    kernel's workgroups at 256 and at 64 with an odd Hkv."""
     ns, sl = ctypes.c_int32(), ctypes.c_int32()
     _lib.call("exkv_plan_splits_hd", B, Hkv, Hq, T, D, ctypes.byref(ns), ctypes.byref(sl))
     return ns.value, sl.value

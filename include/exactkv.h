@@ -350,8 +350,10 @@ int exkv_plan_splits(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t targ
                      int32_t min_split, int32_t* nsplit, int32_t* split_len);
 
 /* The split plan for head dim D (host pointers out): at 128 exkv_plan_splits with its
- * defaults; at 64 and 256 rounds of 512 of the generic-head-dim kernel's workgroups (one
- * per KV head and group of 16 query heads).
+ * defaults; at 64 with an even Hkv the same plan over Hkv / 2 pairs of KV heads (the
+ * attention calls run head dim 64 as pairs of heads with the head-dim-128 kernel
+ * structure); at 256, and 64 with an odd Hkv, rounds of 512 of the generic-head-dim
+ * kernel's workgroups (one per KV head and group of 16 query heads).
  * No counterpart in the reference (head dim 128 only, cache.py:21). */
 int exkv_plan_splits_hd(int32_t B, int32_t Hkv, int32_t Hq, int32_t T, int32_t D, int32_t* nsplit,
                         int32_t* split_len);

@@ -96,6 +96,39 @@ def test_split_plans(D, ns_sl):
     _check(o_c, o_r, q, k, v, T)
 
 
+@pytest.mark.parametrize("B,TS,Hq,Hkv,rate", [(2, 704, 16, 4, 0.2), (1, 1504, 12, 6, 0.05), (2, 912, 32, 16, 0.1),
+                                            (3, 1024, 8, 8, 0.02)])
+def test_pairs_of_heads_raw_rows_and_blocks(B, TS, Hq, Hkv, rate):
+    """Head dim 64 runs as pairs of KV heads: 2, 1 and 4 pairs per workgroup (Hkv 4, 6, 16;
+    4, 8 and 2 page phases), raw rows in K and V of both heads of a pair at rates that put
+    1-4 of a page pair's rows through the ring and more of them through the pool, a ragged
+    last page, with the default plan, one split and 16-token splits: twin bits and the
+    oracle's tolerance."""
+    D, T = 64, TS - 3
+    _say("pairs of heads", B, TS, Hq, Hkv, rate)
+    k = synthetic.make_kv(B, TS, Hkv, D=D, kind="k", seed=Hkv, raw_row_rate=rate)
+    v = synthetic.make_kv(B, TS, Hkv, D=D, kind="v", seed=Hkv + 1, raw_row_rate=rate)
+    q = synthetic.make_q(B, Hq, D=D, seed=Hkv + 2)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    # raw rows per page pair (K and V of heads 2v, 2v+1): 1-4 (through the ring) at the lower
+    # rates, more (from the pool) at the higher ones (all of them at 0.2)
+    rows = (_popc16(kc.rowmask) + _popc16(vc.rowmask)).view(B, TS // 16, Hkv // 2, 2).sum(-1)
+    if rate <= 0.1:
+        assert int(((rows >= 1) & (rows <= 4)).sum()) > 0
+    if rate >= 0.05:
+        assert int((rows > 4).sum()) > 0
+    for ns, sl in ((None, None), (1, TS), (TS // 16, 16)):
+        o_c = kernels.attention_compressed(qd, kc, vc, T, nsplit=ns, split_len=sl)
+        o_r = kernels.attention_reference(qd, kd, vd, T, nsplit=ns, split_len=sl)
+        _check(o_c, o_r, q, k, v, T)
+
+
+def _popc16(t):
+    t = t.to(torch.int32)
+    return sum((t >> i) & 1 for i in range(16))
+
+
 @pytest.mark.parametrize("D", [64, 256])
 def test_lengths_window_and_paged(D):
     """Per-sequence lengths, a sliding window and a block table (pages shuffled over a pool):

@@ -36,6 +36,11 @@
 //     head, so the softmax rescale needs no cross-lane traffic.
 // Everything after the K/V rebuild is shared by the two kernels, so the compressed and
 // uncompressed results are identical bit for bit.
+//
+// Other head dims: 64 with an even number of KV heads runs the same structure over pairs
+// of heads (attn_pair_kernel: a pair has one head-dim-128 head's bytes per token row);
+// 256, and 64 with an odd count, run attn_dgen_kernel (one KV head per workgroup, each
+// wavefront loading its own pages).
 #include <hip/hip_ext.h>
 
 #include "tile.hpp"

@@ -1,0 +1,174 @@
+"""A seeded sweep over the decode-attention configuration space on the GPU: head dims 64,
+128 and 256; GQA ratios from 1 to 32; odd and even KV-head counts (every heads-per-workgroup
+and page-phase count, and the generic kernel for odd counts at head dim 64); one length for
+the batch or one per sequence; sliding windows; the default split plan, one split, and
+explicit split lengths of 1 to 8 pages; paged pools whose unused pages hold NaN and inf;
+raw-row rates from none to every tenth row; the merge in the split kernel's tail at head
+dim 128 (reference kernels.py:142-194 for the split kernels, :33-43 for the merge).
+
+Every case checks:
+  * the compressed call == the bf16 twin bit for bit (same contents, same plan);
+  * the same call through a block table over a shuffled page pool == the contiguous call,
+    for both caches;
+  * each sequence's output within the north-star tolerance (1e-2 relative + 2 bf16 ulp of
+    the row) of the oracle's fp32 and fp64 softmax attention over its window. The
+    reference's absolute 2e-2 bound against fp64 (tests/test_exactkv.py:75-78) is for its
+    unit-scale V; the sweep's V carries per-channel scales, so outputs of a few units (2
+    bf16 ulp above 2e-2) are expected and the relative bound is the one that applies;
+  * the fused merge == the separate merge bit for bit up to 32 splits (within the oracle's
+    tolerance beyond);
+  * decode_to_bf16 of the encoded cache == its source.
+"""
+import numpy as np
+import pytest
+import torch
+
+import exactkv_amd as exactkv
+from exactkv_amd import kernels
+from oracle import attention as oatt
+from tests.conftest import same_bits, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+P = 16
+N_CASES = 256
+
+
+def _cases(seed=20261202):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(N_CASES):
+        D = int(rng.choice([64, 128, 256], p=[0.3, 0.45, 0.25]))
+        Hkv = int(rng.choice([1, 2, 3, 4, 6, 8, 16]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 16, 32]))
+        B = int(rng.integers(1, 5))
+        TS = P * int(rng.integers(1, 65))
+        per_seq = bool(rng.random() < 0.5)
+        lens = [int(x) for x in rng.integers(1, TS + 1, size=B)] if per_seq else None
+        T = TS if per_seq else int(rng.integers(1, TS + 1))
+        window = int(rng.integers(1, TS + 1)) if rng.random() < 0.35 else 0
+        reach = TS if per_seq else T
+        if window:
+            reach = min(reach, window + P - 1)
+        u = rng.random()
+        if u < 0.5:
+            plan = (None, None)
+        elif u < 0.65:
+            plan = (1, -(-reach // P) * P)
+        else:
+            sl = P * int(rng.integers(1, 9))
+            plan = (-(-reach // sl), sl)
+        rate = float(rng.choice([0.0, 0.003, 0.03, 0.1]))
+        fused = D == 128 and bool(rng.random() < 0.4)
+        spare = int(rng.integers(0, 9))
+        out.append(dict(i=i, D=D, Hkv=Hkv, Hq=Hkv * G, B=B, TS=TS, T=T, lens=lens, window=window, plan=plan,
+                        rate=rate, fused=fused, spare=spare, seed=int(rng.integers(1, 2**31))))
+    return out
+
+
+CASES = _cases()
+
+
+def _data(c):
+    """K (per-channel scales, exact zeros, rows forced raw at the case's rate), V, q: CPU seeded."""
+    g = torch.Generator().manual_seed(c["seed"])
+    B, TS, Hkv, D, Hq = c["B"], c["TS"], c["Hkv"], c["D"], c["Hq"]
+    sk = 0.3 + 1.2 * float(torch.rand(1, generator=g))
+    k = torch.randn(B, TS, Hkv, D, generator=g) * torch.exp(torch.randn(Hkv, D, generator=g) * sk)
+    v = torch.randn(B, TS, Hkv, D, generator=g) * torch.exp(torch.randn(Hkv, D, generator=g) * 0.5)
+    k[:, ::97, :, 3] = 0.0
+    v[:, 7::89, :, D - 2] = 0.0
+    for x in (k, v):
+        raw = torch.rand(B, TS, Hkv, generator=g) < c["rate"]
+        ch = torch.randint(0, D, (B, TS, Hkv), generator=g)
+        sel = x.gather(3, ch.unsqueeze(-1)) * 2.0 ** -20
+        x.scatter_(3, ch.unsqueeze(-1), torch.where(raw.unsqueeze(-1), sel, x.gather(3, ch.unsqueeze(-1))))
+    q = torch.randn(B, Hq, D, generator=g) * (0.1 + 0.4 * float(torch.rand(1, generator=g)))
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def _encode(x):
+    B, T, H, D = x.shape
+    c = exactkv.CompressedKV(B, T, H, D, reserve=1.0)
+    st = (x.stride(0), P * x.stride(1), x.stride(1), x.stride(2))
+    kernels.encode_pages(x, st, c._buf(), 0, 0, B, T // P)
+    return c
+
+
+def _pool(x, table, pool_pages, seed):
+    """x's pages placed at table's pool pages; the unused pages hold random values with NaN and
+    inf (attention must never read them)."""
+    B, TS, H, D = x.shape
+    g = torch.Generator().manual_seed(seed)
+    pool = torch.randn(1, pool_pages * P, H, D, generator=g) * 1e4
+    pool[0, ::5, :, 1] = float("nan")
+    pool[0, 3::7, :, 2] = float("inf")
+    pool = pool.to(torch.bfloat16)
+    for b in range(B):
+        for p in range(TS // P):
+            dst = int(table[b, p]) * P
+            pool[0, dst:dst + P] = x[b, p * P:(p + 1) * P]
+    return pool
+
+
+def _label(c):
+    return (f"case {c['i']}: D={c['D']} B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} TS={c['TS']} T={c['T']} "
+            f"lens={c['lens']} window={c['window']} plan={c['plan']} rate={c['rate']} fused={c['fused']}")
+
+
+@pytest.mark.parametrize("c", CASES, ids=[f"case{c['i']}" for c in CASES])
+def test_attention_sweep(c):
+    print("[case]", _label(c), flush=True)
+    B, TS, T, W, D = c["B"], c["TS"], c["T"], c["window"], c["D"]
+    ns, sl = c["plan"]
+    q, k, v = _data(c)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    kc, vc = _encode(kd), _encode(vd)
+    ld = torch.tensor(c["lens"], dtype=torch.int32, device=DEV) if c["lens"] else None
+    kw = dict(lens=ld, nsplit=ns, split_len=sl, window=W)
+
+    o_c = kernels.attention_compressed(qd, kc, vc, T, **kw)
+    o_r = kernels.attention_reference(qd, kd, vd, T, **kw)
+    assert same_bits(o_c, o_r), "compressed != bf16 twin"
+
+    # the oracle over each sequence's window
+    qn, kn, vn = u16(q), u16(k), u16(v)
+    oc = o_c.float().cpu().numpy()
+    for b in range(B):
+        n = c["lens"][b] if c["lens"] else T
+        lo = max(n - W, 0) if W else 0
+        ks, vs = kn[b:b + 1, lo:n], vn[b:b + 1, lo:n]
+        r32 = oatt.attention(qn[b:b + 1], ks, vs, n - lo, np.float32)
+        excess = oatt.tolerance_excess(oc[b:b + 1], r32)
+        assert excess <= 0, f"sequence {b}: outside the bf16 tolerance by {excess:.3g}"
+        r64 = oatt.attention(qn[b:b + 1], ks, vs, n - lo, np.float64)
+        excess = oatt.tolerance_excess(oc[b:b + 1], r64)
+        assert excess <= 0, f"sequence {b}: outside the bf16 tolerance of fp64 by {excess:.3g}"
+
+    # the same pages through a block table over a shuffled pool with garbage pages
+    npg = TS // P
+    pool_pages = B * npg + c["spare"]
+    perm = torch.randperm(pool_pages, generator=torch.Generator().manual_seed(c["seed"] + 1))
+    table = perm[: B * npg].view(B, npg).to(torch.int32)
+    pk_cpu, pv_cpu = _pool(k, table, pool_pages, c["seed"] + 2), _pool(v, table, pool_pages, c["seed"] + 3)
+    pk, pv = pk_cpu.to(DEV), pv_cpu.to(DEV)
+    pkc, pvc = _encode(pk), _encode(pv)
+    td = table.to(DEV)
+    op_c = kernels.attention_compressed(qd, pkc, pvc, T, block_table=td, **kw)
+    op_r = kernels.attention_reference(qd, pk, pv, T, block_table=td, **kw)
+    assert same_bits(op_c, o_c), "paged compressed != contiguous compressed"
+    assert same_bits(op_r, o_c), "paged twin != contiguous compressed"
+
+    if c["fused"]:
+        o_f = kernels.attention_compressed(qd, kc, vc, T, fused_merge=True, **kw)
+        nsplit = ns if ns is not None else kernels._plan(B, c["Hkv"], c["Hq"], T, TS, ld, None, None, W, D)[0]
+        if nsplit <= 32:
+            assert same_bits(o_f, o_c), "fused merge != separate merge"
+        else:
+            for b in range(B):
+                n = c["lens"][b] if c["lens"] else T
+                lo = max(n - W, 0) if W else 0
+                r32 = oatt.attention(qn[b:b + 1], kn[b:b + 1, lo:n], vn[b:b + 1, lo:n], n - lo, np.float32)
+                assert oatt.tolerance_excess(o_f[b:b + 1].float().cpu().numpy(), r32) <= 0
+
+    assert same_bits(kernels.decode_to_bf16(kc, TS), kd)

@@ -172,3 +172,73 @@ def test_attention_sweep(c):
                 assert oatt.tolerance_excess(o_f[b:b + 1].float().cpu().numpy(), r32) <= 0
 
     assert same_bits(kernels.decode_to_bf16(kc, TS), kd)
+
+
+def _cache_cases(seed=7021):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(32):
+        D = int(rng.choice([64, 128, 256]))
+        B = int(rng.integers(1, 7))
+        H = int(rng.choice([1, 2, 3, 4, 8]))
+        TS = P * int(rng.integers(2, 13))
+        T0 = int(rng.integers(0, TS))
+        n = min(TS - T0, int(rng.integers(1, 81)))
+        rate = float(rng.choice([0.0, 0.05, 0.3]))
+        reserve = float(rng.choice([0.0, 0.001, 0.01, 0.5]))
+        out.append(dict(i=i, D=D, B=B, H=H, TS=TS, T0=T0, n=n, rate=rate, reserve=reserve,
+                        seed=int(rng.integers(1, 2**31))))
+    return out
+
+
+CACHE_CASES = _cache_cases()
+
+
+@pytest.mark.parametrize("c", CACHE_CASES, ids=[f"cache{c['i']}" for c in CACHE_CASES])
+def test_cache_sweep(c):
+    """Prefill, then appends across page ends with check_overflow after each (pools started
+    small enough to grow): byte-equal to the CPU model of the protocol (oracle/cache.py;
+    reference cache.py:17-158) at every page end and at the end; the decoded cache and
+    attention over it equal the bf16 cache's (reference tests/test_exactkv.py:81-104)."""
+    from oracle import cache as ocache
+    print("[case]", c, flush=True)
+    B, H, D, TS, T0 = c["B"], c["H"], c["D"], c["TS"], c["T0"]
+    g = torch.Generator().manual_seed(c["seed"])
+
+    def make(n):
+        x = torch.randn(B, n, H, D, generator=g) * torch.exp(torch.randn(H, D, generator=g))
+        x[torch.rand(B, n, H, generator=g) < c["rate"], D // 3] = 1e-30       # forces raw rows
+        return x.to(torch.bfloat16)
+
+    kc = exactkv.CompressedKV(B, TS, H, D, reserve=c["reserve"])
+    tw = exactkv.BF16KV(B, TS, H, D)
+    m = ocache.CacheModel(B, TS, H, D, reserve=c["reserve"])
+
+    def same_state(tag):
+        for k in ("sm", "code", "base", "rowmask", "rowoff"):
+            assert np.array_equal(getattr(kc, k).cpu().numpy(), getattr(m, k)), (tag, k)
+        assert np.array_equal(u16(kc.raw), m.raw), (tag, "raw")
+        assert int(kc.cnt.item()) == m.cnt and kc.cap == m.cap and kc.T == m.T and kc.grows == m.grows, tag
+
+    if T0:
+        x0 = make(T0)
+        x0d = x0.to(DEV)
+        for b in range(B):
+            kc.prefill_slot(b, x0d[b:b + 1].contiguous())
+            tw.prefill_slot(b, x0d[b:b + 1].contiguous())
+            m.prefill_slot(b, u16(x0[b]))
+        same_state("prefill")
+    xs = make(c["n"])
+    xsd = xs.to(DEV)
+    for t in range(c["n"]):
+        kc.append(xsd[:, t].contiguous())
+        tw.append(xsd[:, t].contiguous())
+        m.append(u16(xs[:, t]))
+        exactkv.check_overflow([kc])
+        m.check_overflow()
+        if kc.T % P == 0:
+            same_state(t)
+    same_state("end")
+    assert same_bits(kernels.decode_to_bf16(kc.buffers(), kc.T), tw.buf[:, :kc.T])
+    q = (torch.randn(B, 4 * H, D, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+    assert same_bits(exactkv.decode_attention(q, kc, kc), exactkv.decode_attention(q, tw, tw))

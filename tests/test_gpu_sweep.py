@@ -242,3 +242,100 @@ def test_cache_sweep(c):
     assert same_bits(kernels.decode_to_bf16(kc.buffers(), kc.T), tw.buf[:, :kc.T])
     q = (torch.randn(B, 4 * H, D, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
     assert same_bits(exactkv.decode_attention(q, kc, kc), exactkv.decode_attention(q, tw, tw))
+
+
+def _paged_cases(seed=9103):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(16):
+        max_seqs, max_pages = int(rng.integers(2, 7)), int(rng.integers(2, 9))
+        out.append(dict(i=i, D=int(rng.choice([64, 128, 256])), H=int(rng.choice([1, 2, 3, 4, 8])),
+                        G=int(rng.choice([1, 4, 7])), max_seqs=max_seqs, max_pages=max_pages,
+                        num_pages=int(rng.integers(max_pages, max_seqs * max_pages + 5)),
+                        reserve=float(rng.choice([1e-4, 0.01, 0.5])), ops=150, seed=int(rng.integers(1, 2**31))))
+    return out
+
+
+PAGED_CASES = _paged_cases()
+
+
+@pytest.mark.parametrize("c", PAGED_CASES, ids=[f"paged{c['i']}" for c in PAGED_CASES])
+def test_paged_protocol_sweep(c):
+    """Random operations on one PageTable shared by paged K/V caches and their bf16 twins:
+    prefills of random lengths (0 to the slot capacity), releases, decode steps over random
+    subsets of the live slots in random order (pages opened as tokens fill them), raw-pool
+    growth (small reserves, 5% raw rows) and compact(). After every step the compressed and
+    bf16 paged attention agree bit for bit; every few operations, and at the end, each live
+    slot's tokens decoded through the block table equal the tokens written."""
+    print("[case]", c, flush=True)
+    rng = np.random.Generator(np.random.PCG64(c["seed"]))
+    g = torch.Generator().manual_seed(c["seed"])
+    D, H, Hq = c["D"], c["H"], c["H"] * c["G"]
+    table = exactkv.PageTable(num_pages=c["num_pages"], max_seqs=c["max_seqs"], max_pages=c["max_pages"])
+    kc = exactkv.PagedCompressedKV(table, H, D=D, reserve=c["reserve"])
+    vc = exactkv.PagedCompressedKV(table, H, D=D, reserve=c["reserve"])
+    kb, vb = exactkv.PagedBF16KV(table, H, D=D), exactkv.PagedBF16KV(table, H, D=D)
+    scale = torch.exp(torch.randn(H, D, generator=g))
+    truth = {}
+
+    def tokens(n, k):
+        x = torch.randn(n, H, D, generator=g) * (scale if k else 1.0)
+        x[torch.rand(n, H, generator=g) < 0.05, D // 3] = 1e-30            # raw rows
+        return x.to(torch.bfloat16)
+
+    def check_contents(tag):
+        live = [s for s in table.live_slots() if table.length(s)]
+        if not live:
+            return
+        Tm = max(table.length(s) for s in live)
+        bt = table.block_table.index_select(0, torch.tensor(live, device=DEV))
+        for cache, j in ((kc, 0), (vc, 1)):
+            dec = kernels.decode_to_bf16(cache.buffers(), Tm, block_table=bt)
+            for i, s in enumerate(live):
+                T = table.length(s)
+                assert same_bits(dec[i, :T], torch.stack(truth[s][j]).to(DEV)), (tag, s, j)
+
+    cap = P * c["max_pages"]
+    for op in range(c["ops"]):
+        r = rng.random()
+        free_slots = [s for s in range(c["max_seqs"]) if s not in truth]
+        if r < 0.2 and free_slots:
+            T = int(rng.integers(0, cap + 1))
+            if min(T // P + 1, c["max_pages"]) > table.free_pages():
+                continue
+            s = table.add(T, slot=int(rng.choice(free_slots)))
+            xk, xv = tokens(T, True), tokens(T, False)
+            for cache, x in ((kc, xk), (vc, xv), (kb, xk), (vb, xv)):
+                cache.prefill(s, x.unsqueeze(0).to(DEV).contiguous())
+            truth[s] = [list(xk), list(xv)]
+        elif r < 0.3 and truth:
+            s = int(rng.choice(sorted(truth)))
+            table.release(s)
+            del truth[s]
+        elif r < 0.34 and truth:
+            kc.compact()
+            vc.compact()
+            check_contents(f"compact {op}")
+        else:
+            cand = [s for s in sorted(truth) if table.length(s) < cap]
+            if not cand:
+                continue
+            rows = [int(s) for s in rng.permutation(cand)[: int(rng.integers(1, len(cand) + 1))]]
+            need = sum((table.length(s) + 1) % P == 0 and (table.length(s) + 1) // P < c["max_pages"] for s in rows)
+            if need > table.free_pages():
+                continue
+            table.begin_step(rows)
+            xk, xv = tokens(len(rows), True), tokens(len(rows), False)
+            for i, s in enumerate(rows):
+                truth[s][0].append(xk[i])
+                truth[s][1].append(xv[i])
+            for cache, x in ((kc, xk), (vc, xv), (kb, xk), (vb, xv)):
+                cache.append(x.to(DEV).contiguous())
+            q = (torch.randn(len(rows), Hq, D, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+            o_c = exactkv.decode_attention(q, kc, vc)
+            o_b = exactkv.decode_attention(q, kb, vb)
+            assert same_bits(o_c, o_b), f"op {op}: compressed != bf16 paged attention"
+            exactkv.check_overflow([kc, vc])
+        if op % 10 == 9:
+            check_contents(op)
+    check_contents("end")

@@ -339,3 +339,44 @@ def test_paged_protocol_sweep(c):
         if op % 10 == 9:
             check_contents(op)
     check_contents("end")
+
+
+def _wire_cases(seed=4417):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return [dict(i=i, B=int(rng.integers(1, 5)), H=int(rng.choice([1, 2, 3, 4, 8])), T=int(rng.integers(1, 701)),
+                 rate=float(rng.choice([0.0, 0.01, 0.1])), seed=int(rng.integers(1, 2**31))) for i in range(24)]
+
+
+WIRE_CASES = _wire_cases()
+
+
+@pytest.mark.parametrize("c", WIRE_CASES, ids=[f"wire{c['i']}" for c in WIRE_CASES])
+def test_wire_sweep(c):
+    """Pack every sequence of a cache in one call (sequences in a random order): each blob
+    equals the oracle's (oracle/wire.py) byte for byte; unpacked in another order into a
+    cache whose raw pool must grow, the decoded tokens and the attention bits equal the
+    source cache's."""
+    from exactkv_amd import wire
+    from oracle import wire as owire
+    print("[case]", c, flush=True)
+    B, H, T = c["B"], c["H"], c["T"]
+    g = torch.Generator().manual_seed(c["seed"])
+    x = torch.randn(B, T, H, 128, generator=g) * torch.exp(torch.randn(H, 128, generator=g))
+    x[torch.rand(B, T, H, generator=g) < c["rate"], 11] = 1e-30
+    x = x.to(torch.bfloat16)
+    TS = -(-T // P) * P + P
+    src = exactkv.CompressedKV(B, TS, H, 128, reserve=0.5)
+    for b in range(B):
+        src.prefill_slot(b, x[b:b + 1].to(DEV).contiguous())
+    order = [int(b) for b in np.random.Generator(np.random.PCG64(c["seed"])).permutation(B)]
+    blobs = wire.pack_many(src, order)
+    for b, blob in zip(order, blobs):
+        want = owire.pack(u16(x[b]))
+        got = blob.cpu().numpy()
+        assert got.size == want.size and np.array_equal(got, want), f"sequence {b}"
+    dst = exactkv.CompressedKV(B, TS, H, 128, reserve=1e-5)
+    wire.unpack_many(blobs[::-1], dst, order[::-1])
+    assert dst.T == T
+    assert same_bits(kernels.decode_to_bf16(dst.buffers(), T), x.to(DEV))
+    q = (torch.randn(B, 4 * H, 128, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
+    assert same_bits(exactkv.decode_attention(q, dst, dst), exactkv.decode_attention(q, src, src))

@@ -380,3 +380,74 @@ def test_wire_sweep(c):
     assert same_bits(kernels.decode_to_bf16(dst.buffers(), T), x.to(DEV))
     q = (torch.randn(B, 4 * H, 128, generator=g) * 0.3).to(torch.bfloat16).to(DEV)
     assert same_bits(exactkv.decode_attention(q, dst, dst), exactkv.decode_attention(q, src, src))
+
+
+def _enc_cases(seed=5519):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(40):
+        nb, npg = int(rng.integers(1, 5)), int(rng.integers(1, 13))
+        out.append(dict(i=i, D=int(rng.choice([64, 128, 256])), H=int(rng.integers(1, 9)), nb=nb, npg=npg,
+                        b0=int(rng.integers(0, 3)), pg0=int(rng.integers(0, 4)),
+                        layout=str(rng.choice(["bthd", "bhtd", "heads2"])), cnt0=int(rng.choice([0, 0, 37, 1000])),
+                        small_cap=bool(rng.random() < 0.3), chained=bool(rng.random() < 0.6),
+                        rate=float(rng.choice([0.0, 0.02, 0.2])), nan_page=bool(rng.random() < 0.2),
+                        seed=int(rng.integers(1, 2**31))))
+    return out
+
+
+ENC_CASES = _enc_cases()
+
+
+@pytest.mark.parametrize("c", ENC_CASES, ids=[f"enc{c['i']}" for c in ENC_CASES])
+def test_encoder_sweep(c):
+    """encode_pages (reference kernels.py:216-268, 340-346) of pages [pg0, pg0 + npg) of
+    sequences [b0, b0 + nb) from token-major, head-major and every-other-head strided
+    sources, the counter starting at 0 or not, a pool large enough or not (rows past cap are
+    dropped while the counter advances), chained or three-launch slot scan, head dims 64 /
+    128 / 256, pages of NaN and inf: every written byte equals the oracle's encode of the same
+    pages (rowoff shifted by the counter's start), nothing outside the pages is written, and
+    the counter and 'before' are the oracle's."""
+    from oracle import codec as ocodec
+    print("[case]", c, flush=True)
+    D, H, nb, npg, b0, pg0 = c["D"], c["H"], c["nb"], c["npg"], c["b0"], c["pg0"]
+    T = P * npg
+    g = torch.Generator().manual_seed(c["seed"])
+    Hs = 2 * H if c["layout"] == "heads2" else H
+    x = torch.randn(nb, T, Hs, D, generator=g) * torch.exp(torch.randn(Hs, D, generator=g))
+    x[torch.rand(nb, T, Hs, generator=g) < c["rate"], D // 5] = 1e-30
+    if c["nan_page"]:
+        x[0, :P, 0, 1] = float("nan")
+        x[-1, T - P:, -1, 2] = float("inf")
+    x = x.to(torch.bfloat16)
+    if c["layout"] == "bhtd":
+        src = x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)   # [nb, T, H, D] view, head-major memory
+    elif c["layout"] == "heads2":
+        src = x.to(DEV)[:, :, ::2]
+    else:
+        src = x.to(DEV)
+    want = ocodec.encode(u16(src.contiguous()))
+    n = want["raw"].shape[0]
+    Bc, TS = b0 + nb + 1, P * (pg0 + npg + 1)
+    kc = exactkv.CompressedKV(Bc, TS, H, D, reserve=0.0 if c["small_cap"] else 1.0)
+    kc.cnt.fill_(c["cnt0"])
+    sentinel = torch.full_like(kc.raw, 3.0)
+    kc.raw.copy_(sentinel)
+    st = (src.stride(0), P * src.stride(1), src.stride(1), src.stride(2))
+    fields = ("sm", "code", "base", "rowmask", "rowoff")
+    old = {k: getattr(kc, k).clone() for k in fields}     # the open page 0 is marked already
+    kernels.encode_pages(src, st, kc._buf(), b0, pg0, nb, npg, chained=c["chained"])
+    t0, t1, p0, p1 = P * pg0, P * (pg0 + npg), pg0, pg0 + npg
+    tok, pag = (slice(b0, b0 + nb), slice(t0, t1)), (slice(b0, b0 + nb), slice(p0, p1))
+    wants = dict(want, rowoff=want["rowoff"] + c["cnt0"])
+    for k, sl in (("sm", tok), ("code", tok), ("base", pag), ("rowmask", pag), ("rowoff", pag)):
+        got = getattr(kc, k)
+        assert np.array_equal(got[sl].cpu().numpy(), wants[k]), k
+        rest, prev = got.clone(), old[k].clone()
+        rest[sl] = 0
+        prev[sl] = 0
+        assert torch.equal(rest, prev), f"{k} written outside the encoded pages"
+    assert int(kc.cnt.item()) == c["cnt0"] + n and int(kc._before.item()) == c["cnt0"]
+    lo, hi = min(c["cnt0"], kc.cap), min(c["cnt0"] + n, kc.cap)
+    assert np.array_equal(u16(kc.raw[lo:hi]), want["raw"][: hi - lo])
+    assert same_bits(kc.raw[:lo], sentinel[:lo]) and same_bits(kc.raw[hi:], sentinel[hi:])

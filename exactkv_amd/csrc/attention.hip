@@ -196,6 +196,13 @@ __device__ inline uint32_t lds_addr(const uint8_t* p) {
 __device__ inline void dma16(const void* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
 }
+// Cache pages and raw rows: read once per call, so they stream with the nontemporal hint
+// (nt: no retention in the L2 and the Infinity Cache). Measured at c2a: compressed split
+// kernel 41.2 -> 37.0 us, bf16 twin 45.8 -> 42.1 us; q keeps the default policy (every
+// split of a unit reads it).
+__device__ inline void dma16_stream(const void* g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(lds) : "memory");
+}
 // 4-byte variant: lane L's dword lands at M0 + 4L.
 __device__ inline void dma4(const void* g, uint32_t lds) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds) : "memory");
@@ -290,22 +297,22 @@ __device__ inline void dma_page_bytes(const AttnArgs& a, const DmaLane& o, int64
     if constexpr (COMP) {
         const uint8_t* ksm = a.k.sm + row0 * 128;
         const uint8_t* vsm = a.v.sm + row0 * 128;
-        dma16(ksm + o.sm0, st + CS_KSM);
-        dma16(vsm + o.sm0, st + CS_VSM);
-        dma16(ksm + o.sm1, st + CS_KSM + 1024);
-        dma16(vsm + o.sm1, st + CS_VSM + 1024);
-        dma16(a.k.code + row0 * 64 + o.code, st + CS_KCODE);
-        dma16(a.v.code + row0 * 64 + o.code, st + CS_VCODE);
+        dma16_stream(ksm + o.sm0, st + CS_KSM);
+        dma16_stream(vsm + o.sm0, st + CS_VSM);
+        dma16_stream(ksm + o.sm1, st + CS_KSM + 1024);
+        dma16_stream(vsm + o.sm1, st + CS_VSM + 1024);
+        dma16_stream(a.k.code + row0 * 64 + o.code, st + CS_KCODE);
+        dma16_stream(a.v.code + row0 * 64 + o.code, st + CS_VCODE);
         // base rows: lanes 0-7 K, 8-15 V
         const uint64_t bsrc = basep.pick((lane & 8) != 0) + (uint64_t)page * 128 + o.base;
-        if (lane < 16) dma16((const void*)(uintptr_t)bsrc, st + CS_BASE);
+        if (lane < 16) dma16_stream((const void*)(uintptr_t)bsrc, st + CS_BASE);
     } else {
         const uint8_t* kp = reinterpret_cast<const uint8_t*>(a.kb) + row0 * 256;
         const uint8_t* vp = reinterpret_cast<const uint8_t*>(a.vb) + row0 * 256;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            dma16(kp + o.bf_k[j], st + BS_K + j * 1024);
-            dma16(vp + o.bf_v[j], st + BS_V + j * 1024);
+            dma16_stream(kp + o.bf_k[j], st + BS_K + j * 1024);
+            dma16_stream(vp + o.bf_v[j], st + BS_V + j * 1024);
         }
     }
 }
@@ -331,7 +338,7 @@ __device__ inline void dma_page_raw(int lane, const PageMeta& m, uint32_t raw_st
         const uint64_t rb = rawp.pick(isv);
         if (lane < 16 * n) {
             if (bad) report_error(kErrRawSlot);
-            dma16((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
+            dma16_stream((const void*)(uintptr_t)(rb + (uint64_t)idx * 256 + (uint64_t)(lane & 15) * 16), raw_st);
         }
     }
 }
@@ -1470,7 +1477,7 @@ __device__ inline int dgen_issue(const AttnArgs& a, const DLanes<D, COMP>& o, in
         const bool v = (o.vmask >> i) & 1u;
         const int byte = 1024 * i;                     // the load's array is fixed by its position
         const PairSrc& ps = !COMP ? bf : (byte < G::CODE ? sm : (byte < G::BASE ? code : base));
-        if ((o.act >> i) & 1u) dma16((const void*)(uintptr_t)(ps.pick(v) + o.off[i]), st + 1024u * i);
+        if ((o.act >> i) & 1u) dma16_stream((const void*)(uintptr_t)(ps.pick(v) + o.off[i]), st + 1024u * i);
     }
     int n = G::NDMA;
     if constexpr (COMP) {
@@ -1487,7 +1494,7 @@ __device__ inline int dgen_issue(const AttnArgs& a, const DLanes<D, COMP>& o, in
             const uint8_t* rb = reinterpret_cast<const uint8_t*>(isv ? a.v.raw : a.k.raw);
             if (lane < LPR * nr) {
                 if (bad) report_error(kErrRawSlot);
-                dma16(rb + idx * (2 * D) + (lane % LPR) * 16, raw_st);
+                dma16_stream(rb + idx * (2 * D) + (lane % LPR) * 16, raw_st);
             }
             ++n;
         }
@@ -1938,7 +1945,7 @@ __device__ inline void dma_pair_raw(int lane, const PairMeta& m, uint32_t raw_st
     const int64_t idx = clamp_slot((int64_t)off, (int64_t)rawn.pick(isv), bad);
     if (lane < 8 * n) {
         if (bad) report_error(kErrRawSlot);
-        dma16((const void*)(uintptr_t)(rawp.pick(isv) + (uint64_t)idx * (2 * kDp) + (uint64_t)(lane & 7) * 16), raw_st);
+        dma16_stream((const void*)(uintptr_t)(rawp.pick(isv) + (uint64_t)idx * (2 * kDp) + (uint64_t)(lane & 7) * 16), raw_st);
     }
 }
 

@@ -360,6 +360,7 @@ __device__ inline void q_dma(const AttnArgs& a, int b, int hk, int hg, int gh, i
 // differ by a constant share one register.
 struct LdsLane {
     uint32_t sml, smh, code, base;    // compressed: sm units g and 4+g of row r, code, base
+    uint32_t bw;                      // compressed: the base dword this lane reads for its row (row_bcast)
     uint32_t tw;                      // V tile row r: units 2g (+16: 2g+1, +128: 8+2g, +144: 9+2g)
     uint32_t tr[4];                   // transpose reads of channel blocks nb (+128: nb + 4)
     uint32_t bk[4];                   // bf16 K row r: units 2g, 2g+1, 8+2g, 9+2g
@@ -371,6 +372,9 @@ __device__ inline LdsLane lds_lane_offsets(int r, int g) {
     o.smh = (uint32_t)(r * 128 + 16 * ((4 + g) ^ (r & 7)));
     o.code = (uint32_t)(r * 64 + 16 * (g ^ ((r >> 1) & 3)));
     o.base = (uint32_t)(16 * g);
+    // r = 0-3: K base dword 4g + r (channels 16g + 4r ..), 4-7: K dword 16 + 4g + r - 4
+    // (channels 64 + 16g + 4(r - 4) ..), 8-15: the same dwords of V (row_bcast)
+    o.bw = (uint32_t)(CS_BASE + 128 * (r >> 3) + 64 * ((r >> 2) & 1) + 16 * g + 4 * (r & 3));
     // V tile / staged bf16 V: row r's logical unit u sits at physical unit u ^ ((r & 3) << 1);
     // the XOR only touches bits 1-2 of u, so units 2g+1, 8+2g, 9+2g follow at +16, +128, +144
     o.tw = (uint32_t)(r * 256 + 16 * ((2 * g) ^ ((r & 3) << 1)));
@@ -413,6 +417,159 @@ __device__ inline void stage_bytes(uint32_t sb, const LdsLane& o, int sm_off, in
     const lds_u8* bp = lds_ptr(sb + o.base) + base_off;
     pb.b_lo = lds16(bp);
     pb.b_hi = lds16(bp + 64);
+}
+
+// ---- base bytes through a row broadcast (the head-dim-128 compressed split kernel)
+//
+// The 16 lanes of row g (lanes 16g .. 16g + 15, channel group g) need the same 32 base bytes
+// of K and of V. Instead of every lane reading them (four 16-byte LDS reads of a page, most
+// of the page's LDS read traffic), lane r of the row reads one dword (LdsLane::bw) -- r =
+// 0-3 and 4-7: dwords 0-3 of its group's low and high K runs, 8-11 and 12-15: the same of V
+// -- and the rebuild takes dword i of a run from lane i of its own row with a DPP row
+// broadcast (row_newbcast), which the compiler folds into the exponent add.
+struct StageSC {
+    uint4 sm_lo, sm_hi, code;
+};
+__device__ inline void stage_sm_code(uint32_t sb, const LdsLane& o, int sm_off, int code_off, StageSC& sc) {
+    sc.sm_lo = lds16(lds_ptr(sb + o.sml) + sm_off);
+    sc.sm_hi = lds16(lds_ptr(sb + o.smh) + sm_off);
+    sc.code = lds16(lds_ptr(sb + o.code) + code_off);
+}
+__device__ inline uint32_t stage_base_word(uint32_t sb, const LdsLane& o) {
+    return *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(sb + o.bw));
+}
+
+template <int L>                       // lane L of the row, to every lane of the row
+__device__ __forceinline__ uint32_t row_bcast(uint32_t x) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x150 + L, 0xf, 0xf, false);
+}
+template <bool Z, int L>
+__device__ __forceinline__ void rebuild4_bc(uint32_t s, uint32_t cn, uint32_t bw, uint32_t& o01, uint32_t& o23) {
+    bf16_pairs(s, Z ? exponents(cn, row_bcast<L>(bw)) : cn + row_bcast<L>(bw), o01, o23);
+}
+template <bool Z, bool HIGH, int L0>
+__device__ __forceinline__ void rebuild_run_bc(const uint4& sm, const uint4& code, uint32_t bw, uint32_t out[8]) {
+    constexpr uint32_t m = 0x0F0F0F0Fu;
+    rebuild4_bc<Z, L0 + 0>(sm.x, (HIGH ? code.x >> 4 : code.x) & m, bw, out[0], out[1]);
+    rebuild4_bc<Z, L0 + 1>(sm.y, (HIGH ? code.y >> 4 : code.y) & m, bw, out[2], out[3]);
+    rebuild4_bc<Z, L0 + 2>(sm.z, (HIGH ? code.z >> 4 : code.z) & m, bw, out[4], out[5]);
+    rebuild4_bc<Z, L0 + 3>(sm.w, (HIGH ? code.w >> 4 : code.w) & m, bw, out[6], out[7]);
+}
+// K (V = false) or V values of the lane from its staged bytes; zf = the wavefront's ballot
+// of (bw & 0x80808080) != 0, whose bits 16g + 4q .. 16g + 4q + 3 cover run q (K low, K high,
+// V low, V high): the zero-group fix-up runs for a run when some row flags it.
+template <bool V>
+__device__ __forceinline__ void rebuild_values_bc(const StageSC& sc, uint32_t bw, uint64_t zf, uint32_t out[16]) {
+    constexpr int L_LO = V ? 8 : 0, L_HI = L_LO + 4;
+    constexpr uint64_t rows = 0x000F000F000F000Full;
+    if ((zf & (rows << L_LO)) != 0)
+        rebuild_run_bc<true, false, L_LO>(sc.sm_lo, sc.code, bw, out);
+    else
+        rebuild_run_bc<false, false, L_LO>(sc.sm_lo, sc.code, bw, out);
+    if ((zf & (rows << L_HI)) != 0)
+        rebuild_run_bc<true, true, L_HI>(sc.sm_hi, sc.code, bw, out + 8);
+    else
+        rebuild_run_bc<false, true, L_HI>(sc.sm_hi, sc.code, bw, out + 8);
+}
+
+// ---- V^T straight from the staged bytes (the head-dim-128 compressed split kernel)
+//
+// ds_read_b64_tr_b8 (gfx950): in each 16-lane group, lane L reads 8 bytes; lanes 2k and 2k + 1
+// form row k (16 bytes) of an 8 x 16 byte matrix, and lane i receives byte i of rows 0..7.
+// The P.V MFMA's A operand for channel block nb is V^T: lane (i = lane & 15, kb = lane >> 4)
+// holds V[4kb + j][16nb + i], j = 0..3. With rows 0-3 = tokens 4kb .. 4kb + 3 of one
+// 16-byte segment and rows 4-7 = the same tokens of another, one read gives a lane the
+// sign|mantissa bytes of its 4 tokens in blocks nb and nb + 4 (segments nb and nb + 4 of
+// the sm rows), one the code bytes of two blocks (code byte j holds channel j in its low
+// nibble and j + 64 in its high one, so they serve blocks + 4 too), and one read of the
+// base row (row k = bytes 16k .. 16k + 15) the lane's base byte of all 8 blocks. The
+// rebuild then yields the A operand itself: V makes no bf16 round trip through LDS.
+struct VtLane {
+    uint32_t sm[4], code[2], base;     // stage offsets of the lane's 8-byte reads
+};
+__device__ inline VtLane vt_lane_offsets(int lane) {
+    const int L = lane & 15, kb = lane >> 4, k = L >> 1, h = L & 1;
+    const int t = 4 * kb + (k & 3);                    // token of the lane's row
+    VtLane o;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {                   // sm: segments nb (rows 0-3), nb + 4 (rows 4-7)
+        const int s = nb + 4 * (k >> 2);
+        o.sm[nb] = (uint32_t)(CS_VSM + t * 128 + 16 * (s ^ (t & 7)) + 8 * h);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {                      // code: segments 2c (rows 0-3), 2c + 1 (rows 4-7)
+        const int s = 2 * c + (k >> 2);
+        o.code[c] = (uint32_t)(CS_VCODE + t * 64 + 16 * (s ^ ((t >> 1) & 3)) + 8 * h);
+    }
+    o.base = (uint32_t)(CS_BASE + 128 + 16 * k + 8 * h);
+    return o;
+}
+struct VtBytes {
+    uint32_t sm[8], code[4], base[2];  // sm[nb], code[nb & 3], base[nb >> 2] byte nb & 3
+};
+__device__ inline uint2 lds_tr8(uint32_t a) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((EXKV_LDS v2i*)lds_ptr(a));
+    return make_uint2((uint32_t)v.x, (uint32_t)v.y);
+}
+__device__ inline void stage_vt_bytes(uint32_t sb, const VtLane& o, VtBytes& vb) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        const uint2 s = lds_tr8(sb + o.sm[nb]);
+        vb.sm[nb] = s.x;
+        vb.sm[nb + 4] = s.y;
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint2 s = lds_tr8(sb + o.code[c]);
+        vb.code[2 * c] = s.x;
+        vb.code[2 * c + 1] = s.y;
+    }
+    const uint2 b = lds_tr8(sb + o.base);
+    vb.base[0] = b.x;
+    vb.base[1] = b.y;
+}
+template <bool Z, int NB>
+__device__ __forceinline__ void rebuild_vt_block(const VtBytes& vb, s16x4& out) {
+    const uint32_t cd = vb.code[NB & 3];
+    const uint32_t cn = (NB < 4 ? cd : cd >> 4) & 0x0F0F0F0Fu;
+    const uint32_t b4 = perm_b32(vb.base[NB >> 2], vb.base[NB >> 2], (NB & 3) * 0x01010101u);
+    uint32_t o01, o23;
+    bf16_pairs(vb.sm[NB], Z ? exponents(cn, b4) : cn + b4, o01, o23);
+    out = __builtin_bit_cast(s16x4, make_uint2(o01, o23));
+}
+template <bool Z, int NB0>
+__device__ __forceinline__ void rebuild_vt_run(const VtBytes& vb, s16x4 (&vt)[8]) {
+    rebuild_vt_block<Z, NB0 + 0>(vb, vt[NB0 + 0]);
+    rebuild_vt_block<Z, NB0 + 1>(vb, vt[NB0 + 1]);
+    rebuild_vt_block<Z, NB0 + 2>(vb, vt[NB0 + 2]);
+    rebuild_vt_block<Z, NB0 + 3>(vb, vt[NB0 + 3]);
+}
+// The zero-group fix-up per run (blocks 0-3: channels 0-63, blocks 4-7: 64-127), decided
+// for the wavefront.
+__device__ __forceinline__ void rebuild_vt(const VtBytes& vb, s16x4 (&vt)[8]) {
+    if (__ballot((vb.base[0] & 0x80808080u) != 0u) != 0)
+        rebuild_vt_run<true, 0>(vb, vt);
+    else
+        rebuild_vt_run<false, 0>(vb, vt);
+    if (__ballot((vb.base[1] & 0x80808080u) != 0u) != 0)
+        rebuild_vt_run<true, 4>(vb, vt);
+    else
+        rebuild_vt_run<false, 4>(vb, vt);
+}
+// Tokens of a ragged page past the split's end or before the window read as zero.
+__device__ __forceinline__ void vt_zero_invalid(s16x4 (&vt)[8], int tok0, int end, int wlo) {
+    uint32_t m[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const int t = tok0 + 2 * d;
+        m[d] = (t < end && t >= wlo ? 0x0000FFFFu : 0u) | (t + 1 < end && t + 1 >= wlo ? 0xFFFF0000u : 0u);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        const uint2 d = __builtin_bit_cast(uint2, vt[nb]);
+        vt[nb] = __builtin_bit_cast(s16x4, make_uint2(d.x & m[0], d.y & m[1]));
+    }
 }
 
 __device__ inline void stage_bf16_k(uint32_t sb, const LdsLane& o, uint32_t out[16]) {
@@ -979,6 +1136,7 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
         const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<true>::per_wave);   // this wave's (uniform)
         const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
         const LdsLane lo = lds_lane_offsets(r, g);
+        const VtLane vto = vt_lane_offsets(lane);
         const PairSrc rawp = pair_src((uint64_t)(uintptr_t)a.k.raw, (uint64_t)(uintptr_t)a.v.raw);
         const PairSrc rawn = pair_src((uint64_t)a.k.raw_rows, (uint64_t)a.v.raw_rows);
 
@@ -1070,27 +1228,39 @@ __global__ void __launch_bounds__(kCompThreads) attn_split_kernel<true>(AttnArgs
             const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
             lds_flag_st(&progress[wave], j);
 
-            // V first: its tile is written and its V^T operands read while K is rebuilt, so
-            // that the stage goes back to the loader right after the score MFMAs
-            PageBytes pk, pv;
-            stage_bytes(sb, lo, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
-            stage_bytes(sb, lo, CS_KSM, CS_KCODE, CS_BASE, pk);
+            // every read of the stage up front: V^T by transposing byte reads, K by rows; the
+            // stage goes back to the loader once they have returned (after the score MFMAs)
+            VtBytes vb;
+            stage_vt_bytes(sb, vto, vb);
+            StageSC pk;
+            stage_sm_code(sb, lo, CS_KSM, CS_KCODE, pk);
+            const uint32_t bw = stage_base_word(sb, lo);
             balance_priority(j, other);
             const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
-            uint32_t kd[16], vd[16];
-            rebuild_values(pv, vd);
-            if (mc.mv != 0) {                          // page with raw V rows
-                keep_branch();
-                splice_raw<true>(a, mc, slot, r, g, vd);
-            }
-            if (ragged) {
-                keep_branch();
-                zero_invalid_rows(valid, vd);
-            }
-            write_v_tile(sb, lo, Ring<true>::vtile, vd);     // over the K bytes, read above
             s16x4 vt[8];
-            read_vt(sb, lo, Ring<true>::vtile, vt);
-            rebuild_values(pk, kd);
+            const uint64_t zf = __ballot((bw & 0x80808080u) != 0u);
+            if (mc.mv == 0) {
+                rebuild_vt(vb, vt);
+                if (ragged) {
+                    keep_branch();
+                    vt_zero_invalid(vt, t0 + 4 * g, c.end, c.wlo);
+                }
+            } else {                                   // a page with raw V rows (rare): V by token
+                keep_branch();                         // rows, its raw rows spliced in, transposed
+                StageSC pv;                            // through a bf16 tile over the K bytes
+                stage_sm_code(sb, lo, CS_VSM, CS_VCODE, pv);   // (already in registers)
+                uint32_t vd[16];
+                rebuild_values_bc<true>(pv, bw, zf, vd);
+                splice_raw<true>(a, mc, slot, r, g, vd);
+                if (ragged) {
+                    keep_branch();
+                    zero_invalid_rows(valid, vd);
+                }
+                write_v_tile(sb, lo, Ring<true>::vtile, vd);
+                read_vt(sb, lo, Ring<true>::vtile, vt);
+            }
+            uint32_t kd[16];
+            rebuild_values_bc<false>(pk, bw, zf, kd);
             if (mc.mk != 0) {
                 keep_branch();
                 splice_raw<false>(a, mc, slot, r, g, kd);

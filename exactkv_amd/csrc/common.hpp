@@ -63,13 +63,17 @@ __host__ __device__ inline uint32_t exponents(uint32_t cn, uint32_t base) {
     return (base & 0x7F7F7F7Fu & ~fm) + cn;
 }
 
-template <bool HAS_ZERO_GROUPS>
-__host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t base, uint32_t& out01, uint32_t& out23) {
-    const uint32_t e = HAS_ZERO_GROUPS ? exponents(cn, base) : cn + base;
+// The two bf16 pairs of four channels from their sign|mantissa bytes s and exponents e.
+__host__ __device__ inline void bf16_pairs(uint32_t s, uint32_t e, uint32_t& out01, uint32_t& out23) {
     const uint32_t lo = bfi_b32(0x7F7F7F7Fu, s, e << 7);
     const uint32_t hi = bfi_b32(0x80808080u, s, e >> 1);
     out01 = perm_b32(hi, lo, 0x05010400u);
     out23 = perm_b32(hi, lo, 0x07030602u);
+}
+
+template <bool HAS_ZERO_GROUPS>
+__host__ __device__ inline void rebuild4(uint32_t s, uint32_t cn, uint32_t base, uint32_t& out01, uint32_t& out23) {
+    bf16_pairs(s, HAS_ZERO_GROUPS ? exponents(cn, base) : cn + base, out01, out23);
 }
 
 // ---------------------------------------------------------------- small device utils

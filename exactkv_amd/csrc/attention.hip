@@ -359,7 +359,7 @@ __device__ inline void q_dma(const AttnArgs& a, int b, int hk, int hg, int gh, i
 // an SGPR every LDS access is one v_add plus an immediate offset; accesses whose offsets
 // differ by a constant share one register.
 struct LdsLane {
-    uint32_t sml, smh, code, base;    // compressed: sm units g and 4+g of row r, code, base
+    uint32_t sml, smh, code;          // compressed: sm units g and 4+g of row r, code
     uint32_t bw;                      // compressed: the base dword this lane reads for its row (row_bcast)
     uint32_t tw;                      // V tile row r: units 2g (+16: 2g+1, +128: 8+2g, +144: 9+2g)
     uint32_t tr[4];                   // transpose reads of channel blocks nb (+128: nb + 4)
@@ -371,7 +371,6 @@ __device__ inline LdsLane lds_lane_offsets(int r, int g) {
     o.sml = (uint32_t)(r * 128 + 16 * (g ^ (r & 7)));
     o.smh = (uint32_t)(r * 128 + 16 * ((4 + g) ^ (r & 7)));
     o.code = (uint32_t)(r * 64 + 16 * (g ^ ((r >> 1) & 3)));
-    o.base = (uint32_t)(16 * g);
     // r = 0-3: K base dword 4g + r (channels 16g + 4r ..), 4-7: K dword 16 + 4g + r - 4
     // (channels 64 + 16g + 4(r - 4) ..), 8-15: the same dwords of V (row_bcast)
     o.bw = (uint32_t)(CS_BASE + 128 * (r >> 3) + 64 * ((r >> 2) & 1) + 16 * g + 4 * (r & 3));
@@ -408,16 +407,6 @@ __device__ inline void lds_st16(lds_u8* p, uint32_t a, uint32_t b, uint32_t c, u
 __device__ inline void keep_branch() { asm volatile(""); }
 
 // ---- rebuild K or V of the staged page (lane = token r, channel group g)
-
-__device__ inline void stage_bytes(uint32_t sb, const LdsLane& o, int sm_off, int code_off, int base_off,
-                                   PageBytes& pb) {
-    pb.sm_lo = lds16(lds_ptr(sb + o.sml) + sm_off);
-    pb.sm_hi = lds16(lds_ptr(sb + o.smh) + sm_off);
-    pb.code = lds16(lds_ptr(sb + o.code) + code_off);
-    const lds_u8* bp = lds_ptr(sb + o.base) + base_off;
-    pb.b_lo = lds16(bp);
-    pb.b_hi = lds16(bp + 64);
-}
 
 // ---- base bytes through a row broadcast (the head-dim-128 compressed split kernel)
 //

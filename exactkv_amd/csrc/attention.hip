@@ -424,9 +424,10 @@ __device__ inline void stage_sm_code(uint32_t sb, const LdsLane& o, int sm_off, 
     sc.sm_hi = lds16(lds_ptr(sb + o.smh) + sm_off);
     sc.code = lds16(lds_ptr(sb + o.code) + code_off);
 }
-__device__ inline uint32_t stage_base_word(uint32_t sb, const LdsLane& o) {
-    return *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(sb + o.bw));
+__device__ inline uint32_t stage_base_word(uint32_t sb, uint32_t off) {
+    return *reinterpret_cast<const EXKV_LDS uint32_t*>(lds_ptr(sb + off));
 }
+__device__ inline uint32_t stage_base_word(uint32_t sb, const LdsLane& o) { return stage_base_word(sb, o.bw); }
 
 template <int L>                       // lane L of the row, to every lane of the row
 __device__ __forceinline__ uint32_t row_bcast(uint32_t x) {
@@ -518,33 +519,40 @@ __device__ inline void stage_vt_bytes(uint32_t sb, const VtLane& o, VtBytes& vb)
     vb.base[0] = b.x;
     vb.base[1] = b.y;
 }
-template <bool Z, int NB>
+// PAIR: a pair of head-dim-64 heads as one 128-channel virtual head (attn_pair_kernel). Its
+// code row is the two heads' 32-byte rows, byte j holding channels j (low nibble) and j + 32
+// (high) of its head, so block nb's codes are in segment (nb & 1) | ((nb >> 1) & 2), high
+// nibbles when nb & 2; with one head of 128 channels, segment nb & 3, high when nb >= 4.
+template <bool Z, int NB, bool PAIR>
 __device__ __forceinline__ void rebuild_vt_block(const VtBytes& vb, s16x4& out) {
-    const uint32_t cd = vb.code[NB & 3];
-    const uint32_t cn = (NB < 4 ? cd : cd >> 4) & 0x0F0F0F0Fu;
+    constexpr int SEG = PAIR ? ((NB & 1) | ((NB >> 1) & 2)) : (NB & 3);
+    constexpr bool HIGH = PAIR ? ((NB & 2) != 0) : (NB >= 4);
+    const uint32_t cd = vb.code[SEG];
+    const uint32_t cn = (HIGH ? cd >> 4 : cd) & 0x0F0F0F0Fu;
     const uint32_t b4 = perm_b32(vb.base[NB >> 2], vb.base[NB >> 2], (NB & 3) * 0x01010101u);
     uint32_t o01, o23;
     bf16_pairs(vb.sm[NB], Z ? exponents(cn, b4) : cn + b4, o01, o23);
     out = __builtin_bit_cast(s16x4, make_uint2(o01, o23));
 }
-template <bool Z, int NB0>
+template <bool Z, int NB0, bool PAIR>
 __device__ __forceinline__ void rebuild_vt_run(const VtBytes& vb, s16x4 (&vt)[8]) {
-    rebuild_vt_block<Z, NB0 + 0>(vb, vt[NB0 + 0]);
-    rebuild_vt_block<Z, NB0 + 1>(vb, vt[NB0 + 1]);
-    rebuild_vt_block<Z, NB0 + 2>(vb, vt[NB0 + 2]);
-    rebuild_vt_block<Z, NB0 + 3>(vb, vt[NB0 + 3]);
+    rebuild_vt_block<Z, NB0 + 0, PAIR>(vb, vt[NB0 + 0]);
+    rebuild_vt_block<Z, NB0 + 1, PAIR>(vb, vt[NB0 + 1]);
+    rebuild_vt_block<Z, NB0 + 2, PAIR>(vb, vt[NB0 + 2]);
+    rebuild_vt_block<Z, NB0 + 3, PAIR>(vb, vt[NB0 + 3]);
 }
-// The zero-group fix-up per run (blocks 0-3: channels 0-63, blocks 4-7: 64-127), decided
-// for the wavefront.
+// The zero-group fix-up per run of blocks (0-3, 4-7; their base bytes are base[0], base[1]),
+// decided for the wavefront.
+template <bool PAIR = false>
 __device__ __forceinline__ void rebuild_vt(const VtBytes& vb, s16x4 (&vt)[8]) {
     if (__ballot((vb.base[0] & 0x80808080u) != 0u) != 0)
-        rebuild_vt_run<true, 0>(vb, vt);
+        rebuild_vt_run<true, 0, PAIR>(vb, vt);
     else
-        rebuild_vt_run<false, 0>(vb, vt);
+        rebuild_vt_run<false, 0, PAIR>(vb, vt);
     if (__ballot((vb.base[1] & 0x80808080u) != 0u) != 0)
-        rebuild_vt_run<true, 4>(vb, vt);
+        rebuild_vt_run<true, 4, PAIR>(vb, vt);
     else
-        rebuild_vt_run<false, 4>(vb, vt);
+        rebuild_vt_run<false, 4, PAIR>(vb, vt);
 }
 // Tokens of a ragged page past the split's end or before the window read as zero.
 __device__ __forceinline__ void vt_zero_invalid(s16x4 (&vt)[8], int tok0, int end, int wlo) {
@@ -2029,6 +2037,7 @@ struct PairLane {
     uint32_t sm[4];       // 8-byte pieces: head 2v channels 8g.., 2v+1's, 2v's 32+8g.., 2v+1's
     uint32_t code[2];     // code bytes 8g..8g+7 of head 2v, of 2v+1
     uint32_t base[4];     // base bytes, in the order of sm
+    uint32_t bw;          // the base dword this lane reads for its row (row_bcast)
     uint32_t tw[2];       // V tile row r: units g, 4+g (+128: 8+g, 12+g)
     uint32_t bk[4];       // bf16 K row r: units g, 8+g, 4+g, 12+g
 };
@@ -2045,6 +2054,10 @@ __device__ inline PairLane pair_lane_offsets(int r, int g) {
     o.base[1] = (uint32_t)(64 + 8 * g);
     o.base[2] = (uint32_t)(32 + 8 * g);
     o.base[3] = (uint32_t)(96 + 8 * g);
+    // row g's base dwords in the order the rebuild takes them (b_lo = pieces 0, 1; b_hi =
+    // pieces 2, 3): lane r = 0-7 K dword r, 8-15 V dword r - 8 (piece (r & 7) >> 1, half r & 1)
+    const int pc = (r & 7) >> 1;                       // piece pc: bytes 8g + 64 (pc & 1) + 32 (pc >> 1)
+    o.bw = (uint32_t)(CS_BASE + 128 * (r >> 3) + 8 * g + 64 * (pc & 1) + 32 * (pc >> 1) + 4 * (r & 1));
     o.tw[0] = (uint32_t)(r * 256 + 16 * (g ^ xt));
     o.tw[1] = (uint32_t)(r * 256 + 16 * ((4 + g) ^ xt));
     const int bku[4] = {g, 8 + g, 4 + g, 12 + g};
@@ -2066,6 +2079,15 @@ __device__ inline void stage_bytes_pair(uint32_t sb, const PairLane& o, int sm_o
     pb.code = make_uint4(c0.x, c0.y, c1.x, c1.y);
     pb.b_lo = make_uint4(b0.x, b0.y, b1.x, b1.y);
     pb.b_hi = make_uint4(b2.x, b2.y, b3.x, b3.y);
+}
+
+__device__ inline void stage_sm_code_pair(uint32_t sb, const PairLane& o, int sm_off, int code_off, StageSC& sc) {
+    const uint2 s0 = lds8(lds_ptr(sb + o.sm[0]) + sm_off), s1 = lds8(lds_ptr(sb + o.sm[1]) + sm_off);
+    const uint2 s2 = lds8(lds_ptr(sb + o.sm[2]) + sm_off), s3 = lds8(lds_ptr(sb + o.sm[3]) + sm_off);
+    const uint2 c0 = lds8(lds_ptr(sb + o.code[0]) + code_off), c1 = lds8(lds_ptr(sb + o.code[1]) + code_off);
+    sc.sm_lo = make_uint4(s0.x, s0.y, s1.x, s1.y);
+    sc.sm_hi = make_uint4(s2.x, s2.y, s3.x, s3.y);
+    sc.code = make_uint4(c0.x, c0.y, c1.x, c1.y);
 }
 
 __device__ inline void stage_bf16_k_pair(uint32_t sb, const PairLane& o, uint32_t out[16]) {
@@ -2338,7 +2360,8 @@ __global__ void __launch_bounds__(kCompThreads) attn_pair_kernel<true>(AttnArgs 
         const uint32_t ring = lds_addr(lds) + (uint32_t)(wave * Ring<true>::per_wave);   // this wave's (uniform)
         const uint32_t raw_ring = ring + (uint32_t)(NST * STB);
         const PairLane po = pair_lane_offsets(r, g);
-        const LdsLane lo = lds_lane_offsets(r, g);     // the V^T reads
+        const LdsLane lo = lds_lane_offsets(r, g);     // the V^T reads of pages with raw V rows
+        const VtLane vto = vt_lane_offsets(lane);
         const PairSrc rawp = pair_src((uint64_t)(uintptr_t)ar.k.raw, (uint64_t)(uintptr_t)ar.v.raw);
         const PairSrc rawn = pair_src((uint64_t)ar.k.raw_rows, (uint64_t)ar.v.raw_rows);
 
@@ -2443,26 +2466,39 @@ __global__ void __launch_bounds__(kCompThreads) attn_pair_kernel<true>(AttnArgs 
             const int other = lds_flag_ld(&progress[wave ^ 4]);   // the partner's count: a hint, read unsynchronised
             lds_flag_st(&progress[wave], j);
 
-            // V first: its tile is written and its V^T operands read while K is rebuilt
-            PageBytes pk, pv;
-            stage_bytes_pair(sb, po, CS_VSM, CS_VCODE, CS_BASE + 128, pv);
-            stage_bytes_pair(sb, po, CS_KSM, CS_KCODE, CS_BASE, pk);
+            // every read of the stage up front: V^T by transposing byte reads, K by rows (base
+            // bytes through the row broadcast); the stage goes back after the score MFMAs
+            VtBytes vb;
+            stage_vt_bytes(sb, vto, vb);
+            StageSC pk;
+            stage_sm_code_pair(sb, po, CS_KSM, CS_KCODE, pk);
+            const uint32_t bw = stage_base_word(sb, po.bw);
             balance_priority(j, other);
             const uint32_t slot = raw_ring + (uint32_t)((j & 1) * kRawSlot);
-            uint32_t kd[16], vd[16];
-            rebuild_values(pv, vd);
-            if ((mc.h[0].mv | mc.h[1].mv) != 0u) {      // page with raw V rows
-                keep_branch();
-                splice_pair<true>(ar, mc, slot, r, g, vd);
-            }
-            if (ragged) {
-                keep_branch();
-                zero_invalid_rows(valid, vd);
-            }
-            write_v_tile_pair(sb, po, Ring<true>::vtile, vd);     // over the K bytes, read above
             s16x4 vt[8];
-            read_vt(sb, lo, Ring<true>::vtile, vt);
-            rebuild_values(pk, kd);
+            const uint64_t zf = __ballot((bw & 0x80808080u) != 0u);
+            if ((mc.h[0].mv | mc.h[1].mv) == 0u) {
+                rebuild_vt<true>(vb, vt);
+                if (ragged) {
+                    keep_branch();
+                    vt_zero_invalid(vt, t0 + 4 * g, c.end, c.wlo);
+                }
+            } else {                                   // a page with raw V rows (rare): V by token
+                keep_branch();                         // rows, its raw rows spliced in, transposed
+                PageBytes pv;                          // through a bf16 tile over the K bytes
+                stage_bytes_pair(sb, po, CS_VSM, CS_VCODE, CS_BASE + 128, pv);   // (already in registers)
+                uint32_t vd[16];
+                rebuild_values(pv, vd);
+                splice_pair<true>(ar, mc, slot, r, g, vd);
+                if (ragged) {
+                    keep_branch();
+                    zero_invalid_rows(valid, vd);
+                }
+                write_v_tile_pair(sb, po, Ring<true>::vtile, vd);
+                read_vt(sb, lo, Ring<true>::vtile, vt);
+            }
+            uint32_t kd[16];
+            rebuild_values_bc<false>(pk, bw, zf, kd);
             if ((mc.h[0].mk | mc.h[1].mk) != 0u) {
                 keep_branch();
                 splice_pair<false>(ar, mc, slot, r, g, kd);

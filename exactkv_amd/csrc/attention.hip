@@ -462,6 +462,16 @@ __device__ __forceinline__ void rebuild_values_bc(const StageSC& sc, uint32_t bw
         rebuild_run_bc<false, true, L_HI>(sc.sm_hi, sc.code, bw, out + 8);
 }
 
+// The same for runs of W dwords (head dim 256: W = 8, lanes L .. L + 7 of the row holding
+// the run's base dwords).
+template <bool Z, bool HIGH, int L, int I, int W>
+__device__ __forceinline__ void rebuild_run_bcw(const uint32_t* sm, const uint32_t* code, uint32_t bw, uint32_t* out) {
+    if constexpr (I < W) {
+        rebuild4_bc<Z, L + I>(sm[I], (HIGH ? code[I] >> 4 : code[I]) & 0x0F0F0F0Fu, bw, out[2 * I], out[2 * I + 1]);
+        rebuild_run_bcw<Z, HIGH, L, I + 1, W>(sm, code, bw, out);
+    }
+}
+
 // ---- V^T straight from the staged bytes (the head-dim-128 compressed split kernel)
 //
 // ds_read_b64_tr_b8 (gfx950): in each 16-lane group, lane L reads 8 bytes; lanes 2k and 2k + 1
@@ -555,7 +565,8 @@ __device__ __forceinline__ void rebuild_vt(const VtBytes& vb, s16x4 (&vt)[8]) {
         rebuild_vt_run<false, 4, PAIR>(vb, vt);
 }
 // Tokens of a ragged page past the split's end or before the window read as zero.
-__device__ __forceinline__ void vt_zero_invalid(s16x4 (&vt)[8], int tok0, int end, int wlo) {
+template <int NB>
+__device__ __forceinline__ void vt_zero_invalid(s16x4 (&vt)[NB], int tok0, int end, int wlo) {
     uint32_t m[2];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
@@ -563,7 +574,7 @@ __device__ __forceinline__ void vt_zero_invalid(s16x4 (&vt)[8], int tok0, int en
         m[d] = (t < end && t >= wlo ? 0x0000FFFFu : 0u) | (t + 1 < end && t + 1 >= wlo ? 0xFFFF0000u : 0u);
     }
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
         const uint2 d = __builtin_bit_cast(uint2, vt[nb]);
         vt[nb] = __builtin_bit_cast(s16x4, make_uint2(d.x & m[0], d.y & m[1]));
     }
@@ -1733,6 +1744,122 @@ __device__ inline void dgen_rebuild(const AttnArgs& a, uint32_t st, uint32_t raw
     }
 }
 
+// K of a head-dim-256 page with its base bytes through the row broadcast: lane r of row g
+// reads base dword r of its row's runs (r = 0-7: channels 32g + 4r .., 8-15: 128 + 32g +
+// 4(r - 8) ..), and the rebuild takes dword i of a run from lane i (low run) or 8 + i.
+__device__ inline void dgen256_rebuild_k(const AttnArgs& a, uint32_t st, uint32_t raw_st, const DMeta& m, int r,
+                                         int g, uint32_t (&d)[Run<256>::V]) {
+    using G = DGen<256, true>;
+    constexpr int D = 256, R = Run<D>::R, W = Run<D>::W;
+    uint32_t sm_lo[W], sm_hi[W], code[W];
+    dread<D, R>(st + G::SMK, r, g * R, sm_lo);
+    dread<D, R>(st + G::SMK, r, D / 2 + g * R, sm_hi);
+    dread<D / 2, R>(st + G::CODE, r, g * R, code);
+    const uint32_t bw = stage_base_word(st, (uint32_t)(G::BASE + 128 * (r >> 3) + 32 * g + 4 * (r & 7)));
+    const uint64_t zf = __ballot((bw & 0x80808080u) != 0u);
+    constexpr uint64_t lo_lanes = 0x00FF00FF00FF00FFull;
+    if ((zf & lo_lanes) != 0)
+        rebuild_run_bcw<true, false, 0, 0, W>(sm_lo, code, bw, d);
+    else
+        rebuild_run_bcw<false, false, 0, 0, W>(sm_lo, code, bw, d);
+    if ((zf & (lo_lanes << 8)) != 0)
+        rebuild_run_bcw<true, true, 8, 0, W>(sm_hi, code, bw, d + 2 * W);
+    else
+        rebuild_run_bcw<false, true, 8, 0, W>(sm_hi, code, bw, d + 2 * W);
+    if (m.mk != 0u) {                                  // uniform: raw K rows (dgen_rebuild's splice)
+        keep_branch();
+        const bool take = ((m.mk >> r) & 1u) != 0;
+        uint32_t x[Run<D>::V];
+        if (draw_in_ring(m)) {
+            draw_values<D>(raw_st, min(__builtin_popcount(m.mk & ((1u << r) - 1u)), G::NRAW - 1), g, x);
+        } else {
+            load_row_values_d<D>(a.k.raw + raw_slot(m.mk, m.ok, r, a.k.raw_rows) * D, g, x);
+            wait_vm<0>();
+            settle(x);
+        }
+#pragma unroll
+        for (int i = 0; i < Run<D>::V; ++i) d[i] = take ? x[i] : d[i];
+    }
+}
+
+// V^T of a head-dim-256 page straight from the stage, as in the head-dim-128 kernels
+// (ds_read_b64_tr_b8: rows 0-3 of a read = the lane's 4 tokens in one 16-byte chunk, rows 4-7
+// the same tokens in another). Block nb (channels 16nb .. 16nb + 15) is sm chunk nb, the low
+// (nb < 8) or high nibbles of code chunk nb & 7 (code byte j: channels j and j + 128), and
+// byte nb of the lane's slice of the base row. 8 sm reads (chunks q and q + 8), 4 code reads
+// (chunks 2c and 2c + 1) and 2 base reads (bytes 128b + 16k + i) of 8 bytes per lane.
+struct Vt256Lane {
+    uint32_t sm[8], code[4], base[2];
+};
+struct Vt256Bytes {
+    uint32_t sm[16], code[8], base[4];   // sm[nb], code[nb & 7], base[nb >> 2] byte nb & 3
+};
+__device__ inline Vt256Lane vt256_lane_offsets(int lane) {
+    using G = DGen<256, true>;
+    const int L = lane & 15, kb = lane >> 4, k = L >> 1, h = L & 1, t = 4 * kb + (k & 3);
+    Vt256Lane o;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        o.sm[q] = (uint32_t)(G::SMV + t * 256 + dswz<256>(t, q + 8 * (k >> 2)) * 16 + 8 * h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        o.code[c] = (uint32_t)(G::CODE + 8 * 256 + t * 128 + dswz<128>(t, 2 * c + (k >> 2)) * 16 + 8 * h);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) o.base[b] = (uint32_t)(G::BASE + 256 + 128 * b + 16 * k + 8 * h);
+    return o;
+}
+__device__ inline void stage_vt256_bytes(uint32_t st, const Vt256Lane& o, Vt256Bytes& vb) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const uint2 v = lds_tr8(st + o.sm[q]);
+        vb.sm[q] = v.x;
+        vb.sm[q + 8] = v.y;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint2 v = lds_tr8(st + o.code[c]);
+        vb.code[2 * c] = v.x;
+        vb.code[2 * c + 1] = v.y;
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const uint2 v = lds_tr8(st + o.base[b]);
+        vb.base[2 * b] = v.x;
+        vb.base[2 * b + 1] = v.y;
+    }
+}
+template <bool Z, int NB>
+__device__ __forceinline__ void rebuild_vt256_block(const Vt256Bytes& vb, s16x4& out) {
+    const uint32_t cd = vb.code[NB & 7];
+    const uint32_t cn = (NB < 8 ? cd : cd >> 4) & 0x0F0F0F0Fu;
+    const uint32_t b4 = perm_b32(vb.base[NB >> 2], vb.base[NB >> 2], (NB & 3) * 0x01010101u);
+    uint32_t o01, o23;
+    bf16_pairs(vb.sm[NB], Z ? exponents(cn, b4) : cn + b4, o01, o23);
+    out = __builtin_bit_cast(s16x4, make_uint2(o01, o23));
+}
+template <bool Z, int NB0>
+__device__ __forceinline__ void rebuild_vt256_run(const Vt256Bytes& vb, s16x4 (&vt)[16]) {
+    rebuild_vt256_block<Z, NB0 + 0>(vb, vt[NB0 + 0]);
+    rebuild_vt256_block<Z, NB0 + 1>(vb, vt[NB0 + 1]);
+    rebuild_vt256_block<Z, NB0 + 2>(vb, vt[NB0 + 2]);
+    rebuild_vt256_block<Z, NB0 + 3>(vb, vt[NB0 + 3]);
+    rebuild_vt256_block<Z, NB0 + 4>(vb, vt[NB0 + 4]);
+    rebuild_vt256_block<Z, NB0 + 5>(vb, vt[NB0 + 5]);
+    rebuild_vt256_block<Z, NB0 + 6>(vb, vt[NB0 + 6]);
+    rebuild_vt256_block<Z, NB0 + 7>(vb, vt[NB0 + 7]);
+}
+// The zero-group fix-up per run (blocks 0-7: channels 0-127, 8-15: 128-255), for the wavefront.
+__device__ __forceinline__ void rebuild_vt256(const Vt256Bytes& vb, s16x4 (&vt)[16]) {
+    if (__ballot(((vb.base[0] | vb.base[1]) & 0x80808080u) != 0u) != 0)
+        rebuild_vt256_run<true, 0>(vb, vt);
+    else
+        rebuild_vt256_run<false, 0>(vb, vt);
+    if (__ballot(((vb.base[2] | vb.base[3]) & 0x80808080u) != 0u) != 0)
+        rebuild_vt256_run<true, 8>(vb, vt);
+    else
+        rebuild_vt256_run<false, 8>(vb, vt);
+}
+
 template <int D, bool COMP>
 __global__ void __launch_bounds__(64 * (D >= 256 ? 2 : 4)) attn_dgen_kernel(AttnArgs a) {
     using G = DGen<D, COMP>;
@@ -1805,6 +1932,8 @@ __global__ void __launch_bounds__(64 * (D >= 256 ? 2 : 4)) attn_dgen_kernel(Attn
     const uint32_t tw = tile + (uint32_t)(r * G::TROW + 2 * g * R);                     // V tile row r, low run
     const uint32_t tr = tile + (uint32_t)((4 * g + (r >> 2)) * G::TROW + 8 * (r & 3));  // transposed reads
     const int trow = 4 * g + (r >> 2);                 // twin: the row this lane's transposed reads supply
+    [[maybe_unused]] Vt256Lane vto{};
+    if constexpr (COMP && D == 256) vto = vt256_lane_offsets(lane);
 
     for (int p = pfirst; p < pend; p += NS * G::NPH) {
 #pragma unroll
@@ -1830,22 +1959,42 @@ __global__ void __launch_bounds__(64 * (D >= 256 ? 2 : 4)) attn_dgen_kernel(Attn
             uint32_t kd[G::V];
             s16x4 vt[G::NB];
             if constexpr (COMP) {
-                uint32_t vd[G::V];
-                dgen_rebuild<D, true>(a, st, raw_slot_of(s), meta[s], r, g, vd);
-                if (ragged && !valid) {                // rows outside [wlo, end) read as zero V
-#pragma unroll
-                    for (int i = 0; i < G::V; ++i) vd[i] = 0u;
+                bool tiled = true;                     // V through the bf16 tile
+                if constexpr (D == 256) {
+                    if (meta[s].mv == 0u) {            // uniform: V^T from transposing byte reads
+                        Vt256Bytes vb;
+                        stage_vt256_bytes(st, vto, vb);
+                        rebuild_vt256(vb, vt);
+                        if (ragged) {
+                            keep_branch();
+                            vt_zero_invalid(vt, t0 + 4 * g, end, wlo);
+                        }
+                        tiled = false;
+                    }
                 }
+                if (tiled) {                           // head dim 64, and pages with raw V rows
+                    uint32_t vd[G::V];
+                    dgen_rebuild<D, true>(a, st, raw_slot_of(s), meta[s], r, g, vd);
+                    if (ragged && !valid) {            // rows outside [wlo, end) read as zero V
 #pragma unroll
-                for (int i = 0; i < R / 8; ++i) {      // the two runs of row r into the V tile
-                    lds_st16(lds_ptr(tw) + 16 * i, vd[4 * i], vd[4 * i + 1], vd[4 * i + 2], vd[4 * i + 3]);
-                    lds_st16(lds_ptr(tw) + D + 16 * i, vd[R / 2 + 4 * i], vd[R / 2 + 4 * i + 1],
-                             vd[R / 2 + 4 * i + 2], vd[R / 2 + 4 * i + 3]);
+                        for (int i = 0; i < G::V; ++i) vd[i] = 0u;
+                    }
+#pragma unroll
+                    for (int i = 0; i < R / 8; ++i) {  // the two runs of row r into the V tile
+                        lds_st16(lds_ptr(tw) + 16 * i, vd[4 * i], vd[4 * i + 1], vd[4 * i + 2], vd[4 * i + 3]);
+                        lds_st16(lds_ptr(tw) + D + 16 * i, vd[R / 2 + 4 * i], vd[R / 2 + 4 * i + 1],
+                                 vd[R / 2 + 4 * i + 2], vd[R / 2 + 4 * i + 3]);
+                    }
                 }
-                dgen_rebuild<D, false>(a, st, raw_slot_of(s), meta[s], r, g, kd);
+                if constexpr (D == 256)
+                    dgen256_rebuild_k(a, st, raw_slot_of(s), meta[s], r, g, kd);
+                else
+                    dgen_rebuild<D, false>(a, st, raw_slot_of(s), meta[s], r, g, kd);
+                if (tiled) {
 #pragma unroll
-                for (int nb = 0; nb < G::NB; ++nb)
-                    vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
+                    for (int nb = 0; nb < G::NB; ++nb)
+                        vt[nb] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((EXKV_LDS s16x4*)lds_ptr(tr + 32 * nb));
+                }
             } else {
                 dread<2 * D, 2 * R>(st + G::BK, r, 2 * g * R, kd);
                 dread<2 * D, 2 * R>(st + G::BK, r, D + 2 * g * R, kd + R / 2);

@@ -10,8 +10,9 @@
 // state, and are merged through LDS at the end (one partial per split and query head).
 //
 // Memory pipeline: every page is brought into its wavefront's private LDS ring by a fixed
-// number of direct-to-LDS loads (global_load_lds_dwordx4), rows placed with XOR swizzles
-// chosen so that the later LDS reads are conflict-free. The compiler does not order LDS
+// number of direct-to-LDS loads (global_load_lds_dwordx4 with the nontemporal hint: the
+// bytes are read once per call), rows placed with XOR swizzles chosen so that the later LDS
+// reads are conflict-free. The compiler does not order LDS
 // reads after these loads, so a stage is read only after an explicit s_waitcnt vmcnt(N)
 // of the wavefront that issued them.
 //   * Compressed cache: two more wavefronts per workgroup (loaders) issue every page's 7
@@ -22,18 +23,20 @@
 //   * bf16 twin: each wavefront issues its own pages' 8 loads, one page ahead (2 stages).
 //
 // Per page:
-//   * K and V are rebuilt bit-exactly in VGPRs from the staged bytes (tile.hpp), lane =
-//     token; raw rows are spliced in from the wavefront's raw-row slots, which one more
-//     direct-to-LDS load per page with raw rows fills (issued by the compute wavefront,
-//     which knows the page's metadata).
+//   * K is rebuilt bit-exactly in VGPRs from the staged bytes (lane = token; the page's base
+//     bytes reach the 16 lanes of a row through a DPP row broadcast), V straight into the
+//     P.V operand layout (V^T) from transposing byte reads (ds_read_b64_tr_b8); raw rows are
+//     spliced in from the wavefront's raw-row slots, which one more direct-to-LDS load per
+//     page with raw rows fills (issued by the compute wavefront, which knows the page's
+//     metadata).
 //   * S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (tokens = rows, the G query heads of the
 //     KV head = columns, padded to 16); online softmax in base 2, scores scaled by
 //     D^-1/2 log2(e), p rounded to bf16 for P.V, l summed from fp32 p.
-//   * V goes back to LDS as a bf16 row tile (over the compressed stage's K bytes, already
-//     in registers; the bf16 twin's stage holds that tile as loaded), and
-//     ds_read_b64_tr_b16 reads it as the V^T operand of v_mfma_f32_16x16x16_bf16; the C
-//     layout of S^T is exactly the P^T operand layout, and O^T accumulates with lane =
-//     head, so the softmax rescale needs no cross-lane traffic.
+//   * V^T is the A operand of v_mfma_f32_16x16x16_bf16: the compressed kernel rebuilds it in
+//     that layout (pages with raw V rows go through a bf16 row tile over the stage's K
+//     bytes, already in registers), the bf16 twin reads it from its stage's V rows with
+//     ds_read_b64_tr_b16; the C layout of S^T is exactly the P^T operand layout, and O^T
+//     accumulates with lane = head, so the softmax rescale needs no cross-lane traffic.
 // Everything after the K/V rebuild is shared by the two kernels, so the compressed and
 // uncompressed results are identical bit for bit.
 //

@@ -47,6 +47,7 @@
 #include <hip/hip_ext.h>
 
 #include "tile.hpp"
+#include "stage.hpp"
 #include "../../include/exactkv.h"
 
 #define EXKV_LDS __attribute__((address_space(3)))
@@ -55,7 +56,6 @@ namespace exkv {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -64,11 +64,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kFusedMaxSplits = 1024;   // up to this many splits the split kernel can merge in its tail
 constexpr int kDmaPerPage[2] = {8, 8}; // direct-to-LDS loads per page: bf16; compressed 7 + a raw-row load (pages with raw rows)
 
-// compressed page stage (bytes): K sm 16x128 | K code 16x64 | V sm | V code | K base,
-// V base (128 each); rowmask/rowoff of the wavefront's pages are loaded once, up front
-constexpr int CS_KSM = 0, CS_KCODE = 2048, CS_VSM = 3072, CS_VCODE = 5120, CS_BASE = 6144, CS_BYTES = 6400;
-// bf16 page stage: K rows 16x256 | V rows 16x256
-constexpr int BS_K = 0, BS_V = 4096, BS_BYTES = 8192;
 
 // Raw rows travel with their page through the DMA ring when a page (K and V together)
 // has at most kRawRing of them: one more load per page into the wave's raw slot of the
@@ -261,35 +256,6 @@ __device__ inline void wait_vm_n(int n) {
         wait_vm<0>();
 }
 
-// Per-lane parts of a page's DMA addresses (fixed for the kernel): byte offsets from the
-// page's first row in each array, with the XOR swizzle of the destination applied.
-struct DmaLane {
-    uint32_t sm0, sm1, code, base, bf_k[4], bf_v[4];
-};
-
-template <bool COMP>
-__device__ inline DmaLane dma_lane_offsets(int lane, int64_t rs) {
-    DmaLane o{};
-    if constexpr (COMP) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {                  // sm: 8 rows per load, 16-B segment ^= row & 7
-            const int row = 8 * j + (lane >> 3);
-            const uint32_t off = (uint32_t)(row * rs * 128 + ((lane & 7) ^ (row & 7)) * 16);
-            (j ? o.sm1 : o.sm0) = off;
-        }
-        const int crow = lane >> 2;                    // code: 16 rows, segment ^= (row >> 1) & 3
-        o.code = (uint32_t)(crow * rs * 64 + ((lane & 3) ^ ((crow >> 1) & 3)) * 16);
-        o.base = (uint32_t)((lane & 7) * 16);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {                  // 4 rows of 256 B per load
-            const int row = 4 * j + (lane >> 4);
-            o.bf_k[j] = (uint32_t)(row * rs * 256 + 16 * ((lane & 15) ^ (row & 7)));
-            o.bf_v[j] = (uint32_t)(row * rs * 256 + 16 * ((lane & 15) ^ ((row & 3) << 1)));
-        }
-    }
-    return o;
-}
 
 // Issue the byte loads of one page into stage st (7 for the compressed cache, 8 for bf16).
 // row0: row index of the page's token 0 ((b*TS + 16*pg)*Hkv + hk); page: its page index.
@@ -475,41 +441,8 @@ __device__ __forceinline__ void rebuild_run_bcw(const uint32_t* sm, const uint32
     }
 }
 
-// ---- V^T straight from the staged bytes (the head-dim-128 compressed split kernel)
-//
-// ds_read_b64_tr_b8 (gfx950): in each 16-lane group, lane L reads 8 bytes; lanes 2k and 2k + 1
-// form row k (16 bytes) of an 8 x 16 byte matrix, and lane i receives byte i of rows 0..7.
-// The P.V MFMA's A operand for channel block nb is V^T: lane (i = lane & 15, kb = lane >> 4)
-// holds V[4kb + j][16nb + i], j = 0..3. With rows 0-3 = tokens 4kb .. 4kb + 3 of one
-// 16-byte segment and rows 4-7 = the same tokens of another, one read gives a lane the
-// sign|mantissa bytes of its 4 tokens in blocks nb and nb + 4 (segments nb and nb + 4 of
-// the sm rows), one the code bytes of two blocks (code byte j holds channel j in its low
-// nibble and j + 64 in its high one, so they serve blocks + 4 too), and one read of the
-// base row (row k = bytes 16k .. 16k + 15) the lane's base byte of all 8 blocks. The
-// rebuild then yields the A operand itself: V makes no bf16 round trip through LDS.
-struct VtLane {
-    uint32_t sm[4], code[2], base;     // stage offsets of the lane's 8-byte reads
-};
-__device__ inline VtLane vt_lane_offsets(int lane) {
-    const int L = lane & 15, kb = lane >> 4, k = L >> 1, h = L & 1;
-    const int t = 4 * kb + (k & 3);                    // token of the lane's row
-    VtLane o;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {                   // sm: segments nb (rows 0-3), nb + 4 (rows 4-7)
-        const int s = nb + 4 * (k >> 2);
-        o.sm[nb] = (uint32_t)(CS_VSM + t * 128 + 16 * (s ^ (t & 7)) + 8 * h);
-    }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {                      // code: segments 2c (rows 0-3), 2c + 1 (rows 4-7)
-        const int s = 2 * c + (k >> 2);
-        o.code[c] = (uint32_t)(CS_VCODE + t * 64 + 16 * (s ^ ((t >> 1) & 3)) + 8 * h);
-    }
-    o.base = (uint32_t)(CS_BASE + 128 + 16 * k + 8 * h);
-    return o;
-}
-struct VtBytes {
-    uint32_t sm[8], code[4], base[2];  // sm[nb], code[nb & 3], base[nb >> 2] byte nb & 3
-};
+// ---- V^T straight from the staged bytes (the head-dim-128 compressed split kernel; the
+// lane offsets, the read's layout and the rebuild arithmetic are in stage.hpp)
 __device__ inline uint2 lds_tr8(uint32_t a) {
     typedef int v2i __attribute__((ext_vector_type(2)));
     const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((EXKV_LDS v2i*)lds_ptr(a));
@@ -531,28 +464,6 @@ __device__ inline void stage_vt_bytes(uint32_t sb, const VtLane& o, VtBytes& vb)
     const uint2 b = lds_tr8(sb + o.base);
     vb.base[0] = b.x;
     vb.base[1] = b.y;
-}
-// PAIR: a pair of head-dim-64 heads as one 128-channel virtual head (attn_pair_kernel). Its
-// code row is the two heads' 32-byte rows, byte j holding channels j (low nibble) and j + 32
-// (high) of its head, so block nb's codes are in segment (nb & 1) | ((nb >> 1) & 2), high
-// nibbles when nb & 2; with one head of 128 channels, segment nb & 3, high when nb >= 4.
-template <bool Z, int NB, bool PAIR>
-__device__ __forceinline__ void rebuild_vt_block(const VtBytes& vb, s16x4& out) {
-    constexpr int SEG = PAIR ? ((NB & 1) | ((NB >> 1) & 2)) : (NB & 3);
-    constexpr bool HIGH = PAIR ? ((NB & 2) != 0) : (NB >= 4);
-    const uint32_t cd = vb.code[SEG];
-    const uint32_t cn = (HIGH ? cd >> 4 : cd) & 0x0F0F0F0Fu;
-    const uint32_t b4 = perm_b32(vb.base[NB >> 2], vb.base[NB >> 2], (NB & 3) * 0x01010101u);
-    uint32_t o01, o23;
-    bf16_pairs(vb.sm[NB], Z ? exponents(cn, b4) : cn + b4, o01, o23);
-    out = __builtin_bit_cast(s16x4, make_uint2(o01, o23));
-}
-template <bool Z, int NB0, bool PAIR>
-__device__ __forceinline__ void rebuild_vt_run(const VtBytes& vb, s16x4 (&vt)[8]) {
-    rebuild_vt_block<Z, NB0 + 0, PAIR>(vb, vt[NB0 + 0]);
-    rebuild_vt_block<Z, NB0 + 1, PAIR>(vb, vt[NB0 + 1]);
-    rebuild_vt_block<Z, NB0 + 2, PAIR>(vb, vt[NB0 + 2]);
-    rebuild_vt_block<Z, NB0 + 3, PAIR>(vb, vt[NB0 + 3]);
 }
 // The zero-group fix-up per run of blocks (0-3, 4-7; their base bytes are base[0], base[1]),
 // decided for the wavefront.

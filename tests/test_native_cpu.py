@@ -131,6 +131,22 @@ def test_rebuild_bitmath_exhaustive(tmp_path):
     assert ctypes is not None
 
 
+def test_transposed_v_layout(tmp_path):
+    """The compressed split kernels' V^T operand (csrc/stage.hpp): page bytes placed as the
+    loaders' direct-to-LDS loads place them, ds_read_b64_tr_b8 emulated, rebuilt values
+    against the format rule, for head-dim-128 heads and head-dim-64 pairs
+    (tests/native/vt_check.cpp)."""
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "vt_check"
+    subprocess.run([hipcc, "-O2", "-o", str(exe), os.path.join(ROOT, "tests", "native", "vt_check.cpp")],
+                   check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
+    assert r.returncode == 0, r.stdout
+    assert ", 0 mismatches" in r.stdout
+
+
 def test_engine_module_imports_without_a_gpu():
     import exactkv_amd as exactkv
     from exactkv_amd import engine

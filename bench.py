@@ -211,8 +211,9 @@ def time_graph(fn, n, warmup, copies, per_graph=32):
     graph are the attention calls of one 32-layer decode step (the engine captures a whole
     step); each graph launch itself costs ~25 us on top of its calls, which graphs of 1-4
     calls would charge to every call (c2a: +1.2-2 us per call). Workspaces are
-    allocated by eager calls on the capture stream beforehand; timed with HIP events on
-    the stream the graph is launched on."""
+    allocated by eager calls on the capture stream beforehand; the graph is replayed
+    untimed (at least 8 times, about 10 ms at c2a) before the timed replays; timed with
+    HIP events on the stream the graph is launched on."""
     import torch
     cs = torch.cuda.Stream()
     with torch.cuda.stream(cs):
@@ -226,7 +227,11 @@ def time_graph(fn, n, warmup, copies, per_graph=32):
     torch.cuda.synchronize()
     reps = max(1, -(-n // per_graph))
     with torch.cuda.stream(cs):
-        g.replay()
+        # untimed replays first, as the eager loops have their warmup: the first replays of a
+        # new graph can run a few us per call slower for a few ms (measured at c2a: replays
+        # 3-6 of 16 at 42.7-44.2 against 39.7-40.6 us per call later)
+        for _ in range(max(8, -(-warmup // per_graph))):
+            g.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         gpu_lead()

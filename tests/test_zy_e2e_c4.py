@@ -11,7 +11,11 @@ benchmark's protocol, bench/e2e.py:66-91).
 
 The logits of a step ([B, 128256] bf16) are compared through per-row fingerprints of
 their 16-bit patterns (two weighted sums in wrapping int64 arithmetic), so no step's
-logits need to be kept: storing them all would take about 32 GB."""
+logits need to be kept: storing them all would take about 32 GB. On a mismatch the test
+names the first decode step and rows where the two runs part.
+
+The file is named to run late in the GPU suite (just before the no-alloc entry point's
+tests): it holds the GPU for minutes, and under -x a failure here stops no other test."""
 import gc
 
 import pytest
@@ -66,6 +70,20 @@ def _run(model, backend, B, ids, w, capsys):
     return torch.stack(toks, 1).cpu(), torch.stack(fps).cpu(), grows, T
 
 
+def _where_they_part(tok_b, tok_c, fp_b, fp_c):
+    """The first decode step whose logits differ (fp: [steps, B, 2]), the rows there, and the
+    first token position where the greedy tokens differ (tok: [B, NEW])."""
+    rows = (fp_b != fp_c).any(-1)                      # [steps, B]
+    steps = rows.any(-1).nonzero().flatten().tolist()
+    toks = (tok_b != tok_c).any(0).nonzero().flatten().tolist()
+    if not steps:
+        return f"logits equal at every step; tokens first differ at position {toks[:1]}"
+    s = steps[0]
+    r = rows[s].nonzero().flatten().tolist()
+    return (f"logits first differ at decode step {s} (token position {s + 1}) in {len(r)} rows {r[:8]}; "
+            f"{len(steps)} steps differ; tokens first differ at position {toks[:1]}")
+
+
 def test_c4_llama31_8b_full_workload_tokens_and_logits(capsys):
     from transformers import LlamaConfig, LlamaForCausalLM
     gc.collect()
@@ -96,6 +114,8 @@ def test_c4_llama31_8b_full_workload_tokens_and_logits(capsys):
     tok_c, fp_c, grows_c, T_c = _run(model, "exactkv", B, ids, w, capsys)
     assert T_b == T_c == PROMPT + NEW - 1
     assert tok_b.shape == (B, NEW)
+    if not (torch.equal(tok_b, tok_c) and torch.equal(fp_b, fp_c)):
+        _say(capsys, _where_they_part(tok_b, tok_c, fp_b, fp_c))
     assert torch.equal(tok_b, tok_c), "greedy tokens differ between the bf16 and the compressed cache"
     assert torch.equal(fp_b, fp_c), "logits differ between the bf16 and the compressed cache"
     # the greedy tokens are not degenerate (random weights still give varied argmaxes)

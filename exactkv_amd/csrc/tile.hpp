@@ -1,6 +1,8 @@
 // Page loader and bit-exact rebuild shared by decode attention and decode_to_bf16.
 //
-// Head dim 128 (the tuned kernels); the templates at the end cover every head dim.
+// First the head-dim-128 forms (the row rebuild that pages with raw V rows take in the
+// head-dim-64 pair kernel, raw-row slots and loads), then templates for every head dim
+// (decode_to_bf16 and the generic-head-dim kernel).
 // Lane layout (one wavefront of 64 lanes covers one 16-token page of one KV head):
 //   r = lane % 16   token within the page
 //   g = lane / 16   channel group: channels [16g, 16g+16) and [64+16g, 64+16g+16)
@@ -32,19 +34,6 @@ struct PageBytes {
 };
 
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
-
-// row: this lane's token row index ((b*TS + t)*H + hk); page: ((b*NP + pg)*H + hk).
-__device__ inline void load_page(const CSrc& c, int64_t row, int64_t page, int g, PageBytes& pb) {
-    const uint8_t* s = c.sm + row * 128 + 16 * g;
-    pb.sm_lo = ld16(s);
-    pb.sm_hi = ld16(s + 64);
-    pb.code = ld16(c.code + row * 64 + 16 * g);
-    const uint8_t* bp = c.base + page * 128 + 16 * g;
-    pb.b_lo = ld16(bp);
-    pb.b_hi = ld16(bp + 64);
-    pb.rmask = c.rowmask[page];
-    pb.roff = c.rowoff[page];
-}
 
 // One of the lane's two channel runs: 16 values from four dwords of sm, code and base bytes
 // (codes in the low nibbles for the run 16g.., high nibbles for 64+16g..).
@@ -100,25 +89,6 @@ __device__ inline int64_t raw_slot(uint32_t rmask, int32_t roff, int r, int64_t 
 __device__ inline void load_raw_values(const uint16_t* raw, int64_t slot, int g, uint32_t out[16]) {
     const uint8_t* rp = reinterpret_cast<const uint8_t*>(raw + slot * 128) + 32 * g;
     const uint4 a0 = ld16(rp), a1 = ld16(rp + 16), h0 = ld16(rp + 128), h1 = ld16(rp + 144);
-    out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
-    out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
-    out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;
-    out[12] = h1.x; out[13] = h1.y; out[14] = h1.z; out[15] = h1.w;
-}
-
-// Rebuild, then splice raw rows straight from the pool (reference kernels.py:106-128).
-__device__ inline void rebuild_page(const CSrc& c, const PageBytes& pb, int r, int g, uint32_t out[16]) {
-    rebuild_values(pb, out);
-    if (pb.rmask != 0) {
-        const uint32_t m = (uint32_t)pb.rmask;
-        if ((m >> r) & 1u) load_raw_values(c.raw, raw_slot(m, pb.roff, r, c.raw_rows), g, out);
-    }
-}
-
-// Uncompressed twin: the same 32 values straight from a bf16 [B, TS, H, 128] buffer.
-__device__ inline void load_bf16_row(const uint16_t* buf, int64_t row, int g, uint32_t out[16]) {
-    const uint8_t* p = reinterpret_cast<const uint8_t*>(buf + row * 128) + 32 * g;
-    const uint4 a0 = ld16(p), a1 = ld16(p + 16), h0 = ld16(p + 128), h1 = ld16(p + 144);
     out[0] = a0.x; out[1] = a0.y; out[2] = a0.z; out[3] = a0.w;
     out[4] = a1.x; out[5] = a1.y; out[6] = a1.z; out[7] = a1.w;
     out[8] = h0.x; out[9] = h0.y; out[10] = h0.z; out[11] = h0.w;

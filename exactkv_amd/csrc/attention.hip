@@ -1316,10 +1316,13 @@ __global__ void __launch_bounds__(64) attn_reduce_kernel(const float* po, const 
 // Separate merge of more than 32 splits: workgroup (row, 16-channel chunk) of four
 // wavefronts, so that a row's loads spread over eight workgroups (rows x 8 of them fill
 // the chip where rows alone would use a few CUs). Lane (split group sg = lane / 8, channel
-// pair cp = lane % 8); wavefront w takes a contiguous quarter of the splits, eight at a
-// time, all loads of a batch in flight together; the sums combine over sg by shuffles,
-// then over the wavefronts in order through LDS. Deterministic, so the compressed call and
-// its twin still agree bit for bit.
+// pair cp = lane % 8); wavefront w takes a contiguous quarter of the splits, 64 at a time
+// with every load of a batch (o, m and l) in flight together, in one pass: its sums are
+// kept relative to the largest m it has seen, rescaled when a batch raises it, so no load
+// waits for a first pass over m. Empty splits (m = -inf) weigh 0, and a wavefront whose
+// splits are all empty adds 0. The sums combine over sg by shuffles, then over the
+// wavefronts in order through LDS, each rescaled to the row's largest m. Deterministic,
+// so the compressed call and its twin still agree bit for bit.
 constexpr int kWideWaves = 4, kWideChunk = 16;
 __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const float* po, const float* pm,
                                                                             const float* pl, uint16_t* out, int ns) {
@@ -1330,19 +1333,10 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
     const float* o = po + row * ns * kD + c0 + 2 * cp;
     const float* m = pm + row * ns;
     const float* l = pl + row * ns;
-    __shared__ float smax[kWideWaves];
-    __shared__ float part[kWideWaves][3][8];
-    float mm = -INFINITY;
-    for (int s = threadIdx.x; s < ns; s += 64 * kWideWaves) mm = fmaxf(mm, m[s]);
-    mm = wave_max(mm);
-    if (lane == 0) smax[wave] = mm;
-    __syncthreads();
-    float M = smax[0];
-#pragma unroll
-    for (int w = 1; w < kWideWaves; ++w) M = fmaxf(M, smax[w]);
+    __shared__ float part[kWideWaves][4][8];
     const int per = (ns + kWideWaves - 1) / kWideWaves;
     const int s0 = min(ns, wave * per), s1 = min(ns, s0 + per);
-    float n0 = 0.f, n1 = 0.f, den = 0.f;
+    float n0 = 0.f, n1 = 0.f, den = 0.f, mw = -INFINITY;
     for (int b0 = s0; b0 < s1; b0 += 64) {
         float2 v[8];
         float mv[8], lv[8];
@@ -1353,9 +1347,23 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
             mv[i] = m[s];
             lv[i] = l[s];
         }
+        float mb = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float w = b0 + 8 * i + sg < s1 ? fast_exp2(mv[i] - M) : 0.f;
+            if (b0 + 8 * i + sg >= s1) mv[i] = -INFINITY;
+            mb = fmaxf(mb, mv[i]);
+        }
+        const float mn = fmaxf(mw, wave_max(mb));
+        if (mn != mw) {                                           // uniform; mn > -inf here
+            const float r = fast_exp2(mw - mn);                   // 0 while mw is -inf
+            n0 *= r;
+            n1 *= r;
+            den *= r;
+            mw = mn;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float w = mv[i] == -INFINITY ? 0.f : fast_exp2(mv[i] - mw);
             n0 = __builtin_fmaf(v[i].x, w, n0);
             n1 = __builtin_fmaf(v[i].y, w, n1);
             den = __builtin_fmaf(lv[i], w, den);
@@ -1371,15 +1379,21 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_reduce_wide_kernel(const
         part[wave][0][cp] = n0;
         part[wave][1][cp] = n1;
         part[wave][2][cp] = den;
+        part[wave][3][cp] = mw;
     }
     __syncthreads();
     if (wave == 0 && sg == 0) {
-        float a0 = part[0][0][cp], a1 = part[0][1][cp], dn = part[0][2][cp];
+        float M = part[0][3][cp];
 #pragma unroll
-        for (int w = 1; w < kWideWaves; ++w) {
-            a0 += part[w][0][cp];
-            a1 += part[w][1][cp];
-            dn += part[w][2][cp];
+        for (int w = 1; w < kWideWaves; ++w) M = fmaxf(M, part[w][3][cp]);
+        float a0 = 0.f, a1 = 0.f, dn = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWideWaves; ++w) {
+            const float mwv = part[w][3][cp];
+            const float f = mwv == -INFINITY ? 0.f : fast_exp2(mwv - M);
+            a0 = __builtin_fmaf(part[w][0][cp], f, a0);
+            a1 = __builtin_fmaf(part[w][1][cp], f, a1);
+            dn = __builtin_fmaf(part[w][2][cp], f, dn);
         }
         reinterpret_cast<uint32_t*>(out + row * kD + c0)[cp] = pack_bf16x2(a0 / dn, a1 / dn);
     }

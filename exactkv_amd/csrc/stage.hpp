@@ -1,7 +1,8 @@
 // The compressed page stage of the head-dim-128 split kernels (and of the head-dim-64 pair
 // kernels, whose virtual heads have the same byte layout): where the loader wavefronts'
-// direct-to-LDS loads place a page's bytes, and the per-lane offsets and arithmetic that
-// rebuild V straight into the P.V operand layout from transposing byte reads. Plain
+// direct-to-LDS loads place a page's bytes, the per-lane offsets and arithmetic that
+// rebuild V straight into the P.V operand layout from transposing byte reads, and those
+// that rebuild K rows (and the V rows of pages with raw V rows) from row reads. Plain
 // arithmetic, compiled for the host as well, so that a CPU program can build a stage the
 // way the loads do and check the layout against the format rule.
 //
@@ -105,6 +106,87 @@ __host__ __device__ __forceinline__ void rebuild_vt_run(const VtBytes& vb, s16x4
     rebuild_vt_block<Z, NB0 + 1, PAIR>(vb, vt[NB0 + 1]);
     rebuild_vt_block<Z, NB0 + 2, PAIR>(vb, vt[NB0 + 2]);
     rebuild_vt_block<Z, NB0 + 3, PAIR>(vb, vt[NB0 + 3]);
+}
+
+// ---- per-lane LDS offsets within a stage (fixed for the kernel). With the stage base in
+// an SGPR every LDS access is one v_add plus an immediate offset; accesses whose offsets
+// differ by a constant share one register.
+struct LdsLane {
+    uint32_t sml, smh, code;          // compressed: sm units g and 4+g of row r, code
+    uint32_t bw;                      // compressed: the base dword this lane reads for its row (row_bcast)
+    uint32_t tw;                      // V tile row r: units 2g (+16: 2g+1, +128: 8+2g, +144: 9+2g)
+    uint32_t tr[4];                   // transpose reads of channel blocks nb (+128: nb + 4)
+    uint32_t bk[4];                   // bf16 K row r: units 2g, 2g+1, 8+2g, 9+2g
+};
+
+__host__ __device__ inline LdsLane lds_lane_offsets(int r, int g) {
+    LdsLane o;
+    o.sml = (uint32_t)(r * 128 + 16 * (g ^ (r & 7)));
+    o.smh = (uint32_t)(r * 128 + 16 * ((4 + g) ^ (r & 7)));
+    o.code = (uint32_t)(r * 64 + 16 * (g ^ ((r >> 1) & 3)));
+    // r = 0-3: K base dword 4g + r (channels 16g + 4r ..), 4-7: K dword 16 + 4g + r - 4
+    // (channels 64 + 16g + 4(r - 4) ..), 8-15: the same dwords of V (row_bcast)
+    o.bw = (uint32_t)(CS_BASE + 128 * (r >> 3) + 64 * ((r >> 2) & 1) + 16 * g + 4 * (r & 3));
+    // V tile / staged bf16 V: row r's logical unit u sits at physical unit u ^ ((r & 3) << 1);
+    // the XOR only touches bits 1-2 of u, so units 2g+1, 8+2g, 9+2g follow at +16, +128, +144
+    o.tw = (uint32_t)(r * 256 + 16 * ((2 * g) ^ ((r & 3) << 1)));
+    // transpose read: lane supplies row trow = 4g + r/4, 8-byte half r & 1 of unit
+    // u = 2nb + ((r & 3) >> 1), i.e. physical 2(nb ^ (trow & 3)) + ((r & 3) >> 1) for nb < 4
+    const int trow = 4 * g + (r >> 2), xq = trow & 3, b1 = (r & 3) >> 1;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) o.tr[nb] = (uint32_t)(trow * 256 + 8 * (r & 1) + 16 * (2 * (nb ^ xq) + b1));
+    // bf16 K rows: unit u at u ^ (r & 7)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int u = (j < 2 ? 2 * g : 8 + 2 * g) + (j & 1);
+        o.bk[j] = (uint32_t)(r * 256 + 16 * (u ^ (r & 7)));
+    }
+    return o;
+}
+
+// The 16-byte sm and code reads of a lane's row (K or V) from a stage
+struct StageSC {
+    uint4 sm_lo, sm_hi, code;
+};
+
+// K rows (and V rows on pages with raw V rows) rebuilt from a lane's staged bytes. The 16
+// lanes of one row of a wavefront (one channel group g) need the same 32 base dwords of K
+// and of V: lane r of the row reads one (LdsLane::bw; r = 0-3 and 4-7: dwords 0-3 of its
+// group's low and high K runs, 8-11 and 12-15: the same of V), and the rebuild takes dword
+// i of a run from lane i of its own row. Bc::get<L>() returns lane L's dword: a DPP row
+// broadcast on the GPU (folded by the compiler into the exponent add), an array on the host.
+template <bool Z, int L, class Bc>
+__host__ __device__ __forceinline__ void rebuild4_from(uint32_t s, uint32_t cn, const Bc& bc, uint32_t& o01,
+                                                       uint32_t& o23) {
+    const uint32_t b = bc.template get<L>();
+    bf16_pairs(s, Z ? exponents(cn, b) : cn + b, o01, o23);
+}
+template <bool Z, bool HIGH, int L0, class Bc>
+__host__ __device__ __forceinline__ void rebuild_run_from(const uint4& sm, const uint4& code, const Bc& bc,
+                                                          uint32_t out[8]) {
+    constexpr uint32_t m = 0x0F0F0F0Fu;
+    rebuild4_from<Z, L0 + 0>(sm.x, (HIGH ? code.x >> 4 : code.x) & m, bc, out[0], out[1]);
+    rebuild4_from<Z, L0 + 1>(sm.y, (HIGH ? code.y >> 4 : code.y) & m, bc, out[2], out[3]);
+    rebuild4_from<Z, L0 + 2>(sm.z, (HIGH ? code.z >> 4 : code.z) & m, bc, out[4], out[5]);
+    rebuild4_from<Z, L0 + 3>(sm.w, (HIGH ? code.w >> 4 : code.w) & m, bc, out[6], out[7]);
+}
+// K (V = false) or V values of the lane (out[0..7]: channels 16g.., out[8..15]: 64 + 16g..);
+// zf = the wavefront's ballot of (bw & 0x80808080) != 0, whose bits 16g + 4q .. 16g + 4q + 3
+// cover run q (K low, K high, V low, V high): the zero-group fix-up runs for a run when some
+// row flags it.
+template <bool V, class Bc>
+__host__ __device__ __forceinline__ void rebuild_values_from(const StageSC& sc, const Bc& bc, uint64_t zf,
+                                                             uint32_t out[16]) {
+    constexpr int L_LO = V ? 8 : 0, L_HI = L_LO + 4;
+    constexpr uint64_t rows = 0x000F000F000F000Full;
+    if ((zf & (rows << L_LO)) != 0)
+        rebuild_run_from<true, false, L_LO>(sc.sm_lo, sc.code, bc, out);
+    else
+        rebuild_run_from<false, false, L_LO>(sc.sm_lo, sc.code, bc, out);
+    if ((zf & (rows << L_HI)) != 0)
+        rebuild_run_from<true, true, L_HI>(sc.sm_hi, sc.code, bc, out + 8);
+    else
+        rebuild_run_from<false, true, L_HI>(sc.sm_hi, sc.code, bc, out + 8);
 }
 
 }  // namespace exkv

@@ -147,6 +147,22 @@ def test_transposed_v_layout(tmp_path):
     assert ", 0 mismatches" in r.stdout
 
 
+def test_row_rebuild_layout(tmp_path):
+    """The compressed split kernel's K rows (and the V rows of pages with raw V rows), from
+    the same stage placement: row reads and base dwords at lds_lane_offsets, the base dwords
+    taken from the lane's own 16-lane row as the DPP row broadcast does, against the format
+    rule (tests/native/krow_check.cpp)."""
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = tmp_path / "krow_check"
+    subprocess.run([hipcc, "-O2", "-o", str(exe), os.path.join(ROOT, "tests", "native", "krow_check.cpp")],
+                   check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    r = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
+    assert r.returncode == 0, r.stdout
+    assert ", 0 mismatches" in r.stdout
+
+
 def test_engine_module_imports_without_a_gpu():
     import exactkv_amd as exactkv
     from exactkv_amd import engine

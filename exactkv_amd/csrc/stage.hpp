@@ -189,4 +189,56 @@ __host__ __device__ __forceinline__ void rebuild_values_from(const StageSC& sc, 
         rebuild_run_from<false, true, L_HI>(sc.sm_hi, sc.code, bc, out + 8);
 }
 
+// Per-lane LDS offsets of the pair layout within a stage (the loader's swizzles: sm rows
+// of 128 bytes with 16-byte unit u at u ^ (r & 7), code rows of 64 bytes with unit u at
+// u ^ ((r >> 1) & 3), base unswizzled, V tile and staged bf16 V rows with unit u at
+// u ^ ((r & 3) << 1), bf16 K rows with unit u at u ^ (r & 7)).
+struct PairLane {
+    uint32_t sm[4];       // 8-byte pieces: head 2v channels 8g.., 2v+1's, 2v's 32+8g.., 2v+1's
+    uint32_t code[2];     // code bytes 8g..8g+7 of head 2v, of 2v+1
+    uint32_t base[4];     // base bytes, in the order of sm
+    uint32_t bw;          // the base dword this lane reads for its row (row_bcast)
+    uint32_t tw[2];       // V tile row r: units g, 4+g (+128: 8+g, 12+g)
+    uint32_t bk[4];       // bf16 K row r: units g, 8+g, 4+g, 12+g
+};
+
+__host__ __device__ inline PairLane pair_lane_offsets(int r, int g) {
+    PairLane o;
+    const int x7 = r & 7, xc = (r >> 1) & 3, xt = (r & 3) << 1, half = 8 * (g & 1), gu = g >> 1;
+    const int smu[4] = {gu, 4 + gu, 2 + gu, 6 + gu};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.sm[i] = (uint32_t)(r * 128 + 16 * (smu[i] ^ x7) + half);
+    o.code[0] = (uint32_t)(r * 64 + 16 * (gu ^ xc) + half);
+    o.code[1] = (uint32_t)(r * 64 + 16 * ((2 + gu) ^ xc) + half);
+    o.base[0] = (uint32_t)(8 * g);
+    o.base[1] = (uint32_t)(64 + 8 * g);
+    o.base[2] = (uint32_t)(32 + 8 * g);
+    o.base[3] = (uint32_t)(96 + 8 * g);
+    // row g's base dwords in the order the rebuild takes them (b_lo = pieces 0, 1; b_hi =
+    // pieces 2, 3): lane r = 0-7 K dword r, 8-15 V dword r - 8 (piece (r & 7) >> 1, half r & 1)
+    const int pc = (r & 7) >> 1;                       // piece pc: bytes 8g + 64 (pc & 1) + 32 (pc >> 1)
+    o.bw = (uint32_t)(CS_BASE + 128 * (r >> 3) + 8 * g + 64 * (pc & 1) + 32 * (pc >> 1) + 4 * (r & 1));
+    o.tw[0] = (uint32_t)(r * 256 + 16 * (g ^ xt));
+    o.tw[1] = (uint32_t)(r * 256 + 16 * ((4 + g) ^ xt));
+    const int bku[4] = {g, 8 + g, 4 + g, 12 + g};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.bk[j] = (uint32_t)(r * 256 + 16 * (bku[j] ^ x7));
+    return o;
+}
+
+// A pair lane's row pieces into the row rebuild's registers: rd(lane offset, array offset)
+// returns the 8 stage bytes at their sum (an LDS read on the GPU, the array offset an
+// immediate); sm pieces in the order head 2v channels 8g.., 2v+1's, 2v's 32 + 8g.., 2v+1's,
+// code pieces head 2v's then 2v+1's.
+template <class R8>
+__host__ __device__ __forceinline__ void stage_sm_code_pair_from(const R8& rd, const PairLane& o, int sm_off,
+                                                                 int code_off, StageSC& sc) {
+    const uint2 s0 = rd(o.sm[0], sm_off), s1 = rd(o.sm[1], sm_off);
+    const uint2 s2 = rd(o.sm[2], sm_off), s3 = rd(o.sm[3], sm_off);
+    const uint2 c0 = rd(o.code[0], code_off), c1 = rd(o.code[1], code_off);
+    sc.sm_lo = make_uint4(s0.x, s0.y, s1.x, s1.y);
+    sc.sm_hi = make_uint4(s2.x, s2.y, s3.x, s3.y);
+    sc.code = make_uint4(c0.x, c0.y, c1.x, c1.y);
+}
+
 }  // namespace exkv

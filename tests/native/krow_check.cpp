@@ -8,6 +8,11 @@
 // source (the DPP row broadcast of the GPU build). Lane (r, g) must hold token r's channels
 // 16g + 2k, 16g + 2k + 1 in out[k] (k < 8) and 64 + 16g + 2(k - 8), + 1 in out[k] (k >= 8).
 // Also with the fix-up forced on every run, and with it off on pages without flagged groups.
+// Then the head-dim-64 pair kernel's K rows (two heads 2v, 2v + 1 of 64 channels as one
+// 128-byte virtual row, each head's code row of 32 bytes holding channels j and j + 32):
+// lane (r, g) reads its pieces at pair_lane_offsets(r, g) through stage_sm_code_pair_from and
+// must hold head 2v channels 8g.. in out[0..3], head 2v + 1's in out[4..7], head 2v channels
+// 32 + 8g.. in out[8..11] and head 2v + 1's in out[12..15].
 #include "../../exactkv_amd/csrc/stage.hpp"
 #include <cstdio>
 #include <cstring>
@@ -120,6 +125,51 @@ static void fill(Arr& a, Rng& rng, int rs, int mode) {
     }
 }
 
+// Pair layout: virtual channel 64h + c is head 2v + h's channel c (c < 64)
+static uint16_t expect_pair(const Page& p, int t, int h, int c) {
+    const size_t row = (size_t)t * p.rs + p.hk;
+    const uint32_t code = (p.k.code[row * 64 + 32 * h + (c & 31)] >> (c >= 32 ? 4 : 0)) & 15;
+    return scalar_decode(p.k.sm[row * 128 + 64 * h + c], code, p.k.base[(size_t)p.hk * 128 + 64 * h + c]);
+}
+
+static long check_pair(const Page& p, const uint8_t* st, int force, bool* flagged) {
+    uint32_t bw[64];
+    uint64_t zf = 0;
+    for (int lane = 0; lane < 64; ++lane) {
+        const PairLane o = pair_lane_offsets(lane & 15, lane >> 4);
+        memcpy(&bw[lane], st + o.bw, 4);
+        if ((bw[lane] & 0x80808080u) != 0u) zf |= 1ull << lane;
+    }
+    if (flagged) *flagged = zf != 0;
+    const uint64_t z = force < 0 ? zf : (force ? ~0ull : 0ull);
+    auto rd = [&](uint32_t off, int arr) {
+        uint2 v;
+        memcpy(&v, st + off + arr, 8);
+        return v;
+    };
+    long bad = 0;
+    for (int lane = 0; lane < 64; ++lane) {
+        const int r = lane & 15, g = lane >> 4;
+        const PairLane o = pair_lane_offsets(r, g);
+        StageSC sc;
+        stage_sm_code_pair_from(rd, o, CS_KSM, CS_KCODE, sc);
+        uint32_t out[16];
+        rebuild_values_from<false>(sc, HostRow{bw + 16 * g}, z, out);
+        for (int k = 0; k < 16; ++k)
+            for (int x = 0; x < 2; ++x) {
+                const int h = (k >> 2) & 1, c = (k >= 8 ? 32 : 0) + 8 * g + 2 * (k & 3) + x;
+                const uint16_t got = (uint16_t)(out[k] >> (16 * x)), want = expect_pair(p, r, h, c);
+                if (got != want) {
+                    if (bad < 4)
+                        printf("  pair lane %d token %d head %d channel %d: got %04x want %04x\n", lane, r, h, c, got,
+                               want);
+                    ++bad;
+                }
+            }
+    }
+    return bad;
+}
+
 int main() {
     Rng rng{0x9E3779B97F4A7C15ull};
     long bad = 0, pages = 0, flagged = 0, plain = 0;
@@ -148,6 +198,24 @@ int main() {
             bad += b0 + b1 + b2;
             ++pages;
         }
+    }
+    // head-dim-64 pairs: the same stage placement (a virtual head's rows are the pair's)
+    for (int trial = 0; trial < 200; ++trial) {
+        Page p;
+        p.rs = shapes[trial & 3][0];
+        p.hk = shapes[trial & 3][1];
+        fill(p.k, rng, p.rs, (trial >> 2) % 4);
+        fill(p.v, rng, p.rs, 0);
+        static uint8_t st[CS_BYTES];
+        memset(st, 0xC3, sizeof st);
+        place(p, st);
+        bool any = false;
+        const long b0 = check_pair(p, st, -1, &any), b1 = check_pair(p, st, 1, nullptr);
+        const long b2 = any ? 0 : check_pair(p, st, 0, nullptr);
+        (any ? flagged : plain) += 1;
+        if (b0 || b1 || b2) printf("pair trial %d (rs %d pair %d): %ld %ld %ld\n", trial, p.rs, p.hk, b0, b1, b2);
+        bad += b0 + b1 + b2;
+        ++pages;
     }
     printf("checked %ld page rebuilds (%ld with flagged base bytes, %ld without), %ld mismatches\n", pages, flagged,
            plain, bad);

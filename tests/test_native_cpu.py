@@ -148,10 +148,10 @@ def test_transposed_v_layout(tmp_path):
 
 
 def test_row_rebuild_layout(tmp_path):
-    """The compressed split kernel's K rows (and the V rows of pages with raw V rows), from
-    the same stage placement: row reads and base dwords at lds_lane_offsets, the base dwords
-    taken from the lane's own 16-lane row as the DPP row broadcast does, against the format
-    rule (tests/native/krow_check.cpp)."""
+    """The compressed split kernel's K rows (and the V rows of pages with raw V rows), and the
+    head-dim-64 pair kernel's K rows, from the same stage placement: row reads and base dwords
+    at lds_lane_offsets / pair_lane_offsets, the base dwords taken from the lane's own 16-lane
+    row as the DPP row broadcast does, against the format rule (tests/native/krow_check.cpp)."""
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not available")

@@ -1,6 +1,8 @@
 """CPU-side checks of the native library (no kernel launches): it loads, exports every
-entry point include/exactkv.h declares, validates arguments before touching the GPU, and
-the value-rebuild bit logic is exact on every (sign|mantissa, code, base) combination."""
+entry point include/exactkv.h declares, validates arguments before touching the GPU, the
+value-rebuild bit logic is exact on every (sign|mantissa, code, base) combination, and the
+split kernels' stage layouts (V^T operands, K and V rows, head-dim-64 pairs) rebuild every
+value by the format rule, compiled for the host from the kernels' own header."""
 import ctypes
 import os
 import re

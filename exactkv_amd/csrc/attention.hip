@@ -914,6 +914,20 @@ constexpr int kCompThreads = 64 * (kWaves + kLoaders);
 constexpr int kLoadAhead = 3;                    // pages a loader keeps in flight besides the newest
 constexpr int kBytesLoads = kDmaPerPage[1] - 1;  // byte loads per compressed page
 static_assert((kLoadAhead + 1) * kBytesLoads <= 63, "a loader's loads in flight must fit vmcnt");
+static_assert(kLoadAhead == 3, "loader_wait_pages covers 0 to kLoadAhead newer pages");
+
+// Wait until a loader's oldest page in flight has landed, k pages (each kBytesLoads loads)
+// being newer than it: the loads of one wavefront land in order.
+__device__ inline void loader_wait_pages(int k) {
+    if (k >= 3)
+        wait_vm<3 * kBytesLoads>();
+    else if (k == 2)
+        wait_vm<2 * kBytesLoads>();
+    else if (k == 1)
+        wait_vm<kBytesLoads>();
+    else
+        wait_vm<0>();
+}
 
 
 // Loader wavefront l (see above)
@@ -950,8 +964,10 @@ __device__ __forceinline__ void comp_loader(const AttnArgs& a, const SplitCoords
             if (lp >= c.pend) continue;
             const int w = w0 + i;
             if (lds_flag_ld(&avail[w]) <= j) {         // its stage is still in use: publish all, then wait
-                wait_vm<0>();
-                while (inflight > 0) publish();
+                while (inflight > 0) {                 // each page as soon as its own loads have landed
+                    loader_wait_pages(inflight - 1);
+                    publish();
+                }
                 int s = 0;
                 for (; s < a.spin && lds_flag_ld(&avail[w]) <= j; ++s) __builtin_amdgcn_s_sleep(1);
                 if (s == a.spin) report_error(kErrWait);
@@ -970,8 +986,10 @@ __device__ __forceinline__ void comp_loader(const AttnArgs& a, const SplitCoords
             }
         }
     }
-    wait_vm<0>();
-    while (inflight > 0) publish();
+    while (inflight > 0) {                             // the last pages, each as soon as it has landed
+        loader_wait_pages(inflight - 1);
+        publish();
+    }
 }
 
 template <>
